@@ -1,0 +1,152 @@
+/*
+ * zk_api.h - C ABI of libzenith_hip.so, the MI355X (gfx950) kernel library
+ * behind the `zenith_cuda` drop-in (relu, gelu, layernorm, matmul,
+ * flash_attention, wmma_matmul) and the fused BERT-encoder epilogues.
+ *
+ * Conventions (all entry points):
+ *   - return int: ZK_OK (0) on success, a negative zk_status on failure;
+ *     zk_last_error() then holds a message (thread-local).
+ *   - every data pointer is a device pointer; sizes and leading dimensions
+ *     are in elements; matrices are row-major.
+ *   - the last argument is the HIP stream (hipStream_t passed as void*; NULL
+ *     means the null stream). Launches are asynchronous; nothing is
+ *     allocated and nothing synchronises inside the library.
+ *   - no torch / C++ types cross this boundary.
+ *
+ * Each declaration cites the reference interface it replaces
+ * (paths relative to the vibeswithkk/ZENITH source tree).
+ */
+#ifndef ZK_API_H
+#define ZK_API_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  ZK_OK = 0,
+  ZK_ERR_INVALID = -1,     /* bad pointer / negative size / bad enum value   */
+  ZK_ERR_UNSUPPORTED = -2, /* valid request this library does not implement */
+  ZK_ERR_HIP = -3          /* a HIP runtime call (launch) failed             */
+} zk_status;
+
+typedef enum { ZK_F32 = 0, ZK_F16 = 1, ZK_I8 = 2, ZK_I32 = 3 } zk_dtype;
+
+/* GELU flavour: tanh approximation (reference CUDA kernels) or exact erf
+ * (BERT / ONNX Gelu with Erf). */
+typedef enum { ZK_GELU_TANH = 0, ZK_GELU_ERF = 1 } zk_gelu_mode;
+
+/* GEMM epilogue applied to the fp32 (or dequantised int32) accumulator.
+ * bias is a length-N vector of the output dtype (fp32 for fp32 output),
+ * residual an [M, N] matrix of the output dtype with leading dim ldr. */
+typedef enum {
+  ZK_EPI_NONE = 0,
+  ZK_EPI_BIAS = 1,
+  ZK_EPI_BIAS_GELU_ERF = 2,
+  ZK_EPI_BIAS_GELU_TANH = 3,
+  ZK_EPI_BIAS_RESIDUAL = 4,
+  ZK_EPI_BIAS_RELU = 5
+} zk_epilogue;
+
+/* Library information. */
+const char *zk_last_error(void);
+int zk_version(void);
+
+/* y = max(x, 0), n elements, dtype ZK_F32 or ZK_F16. x may equal y.
+ * Replaces zenith_cuda.relu: core/bindings/cuda_bindings.cpp:39-46 ->
+ * relu_f32 core/src/cuda_kernels.cu:504-507. */
+int zk_relu(const void *x, void *y, int64_t n, int dtype, void *stream);
+
+/* y[r, c] = GELU(x[r, c] + bias[c]); bias may be NULL. rows*cols elements,
+ * contiguous. dtype ZK_F32 or ZK_F16 (fp32 math either way).
+ * Replaces zenith_cuda.gelu (cuda_bindings.cpp:48-56 -> cuda_kernels.cu:
+ * 115-126, 559-562) and the bias+GELU epilogue fused_bias_gelu
+ * (core/src/fused_kernels.cu:47-62, 347-353). */
+int zk_gelu(const void *x, const void *bias, void *y, int64_t rows,
+            int64_t cols, int mode, int dtype, void *stream);
+
+/* y = LayerNorm(x [+ residual]) * gamma + beta over the last dim (hidden),
+ * population variance, fp32 statistics. residual may be NULL; x, residual, y
+ * are [rows, hidden] contiguous in dtype; gamma/beta are [hidden] in dtype.
+ * Replaces zenith_cuda.layernorm (cuda_bindings.cpp:58-71 ->
+ * cuda_kernels.cu:132-184, 564-575) and fused_add_layernorm
+ * (fused_kernels.cu:145-221, 393-399; CPU form
+ * python/src/features_bindings.hpp:116-171). */
+int zk_layernorm(const void *x, const void *residual, const void *gamma,
+                 const void *beta, void *y, int64_t rows, int64_t hidden,
+                 float eps, int dtype, void *stream);
+
+/* Out-of-place transpose of a [rows, cols] fp16 matrix (leading dim lds)
+ * into [cols, rows] (leading dim ldd). Used to present B[K,N] as the
+ * K-major operand the MFMA GEMM reads.
+ * Replaces the layout shuffles transpose_0213 (cuda_kernels.cu:623-678). */
+int zk_transpose_f16(const void *src, void *dst, int64_t rows, int64_t cols,
+                     int64_t lds, int64_t ldd, void *stream);
+
+/* FP16 GEMM on MFMA, fp32 accumulation:
+ *   C[M,N] = epilogue(A[M,K] . op(B))
+ *   trans_b = 1: B is W[N,K] (torch Linear layout), op(B) = W^T;
+ *   trans_b = 0: B is [K,N] row-major (wmma_matmul layout).
+ * out_dtype ZK_F32 or ZK_F16; bias/residual as in zk_epilogue (may be NULL
+ * for ZK_EPI_NONE). A, B, C must not alias.
+ * Replaces zenith_cuda.wmma_matmul (cuda_bindings.cpp:110-132 ->
+ * cuda_kernels.cu:698-767) and the Linear+GELU epilogue
+ * fused_gemm_epilogue_gelu (fused_kernels.cu:317-330, 416-420). */
+int zk_gemm_f16(const void *A, const void *B, void *C, int64_t M, int64_t N,
+                int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_b,
+                int out_dtype, const void *bias, const void *residual,
+                int64_t ldr, int epilogue, void *stream);
+
+/* FP32 GEMM, C[M,N] = A[M,K] . op(B), trans_b as above, fp32 throughout.
+ * Replaces zenith_cuda.matmul (cuda_bindings.cpp:73-88 ->
+ * matmul_f32 cuda_kernels.cu:297-336, 524-528). */
+int zk_gemm_f32(const float *A, const float *B, float *C, int64_t M,
+                int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
+                int trans_b, void *stream);
+
+/* Flash-attention forward, non-causal, online softmax with fp32 statistics.
+ *   O[b,h,s,:] = softmax(scale * Q[b,h,s,:] . K[b,h,:,:]^T) . V[b,h,:,:]
+ * Tensors are addressed by strides (elements): strides[0..2] are the
+ * (batch, head, seq) strides of Q, [3..5] of K, [6..8] of V, [9..11] of O;
+ * the head_dim axis is contiguous. head_dim in {64, 128}.
+ * valid_lens (int32 [B], may be NULL): keys j >= valid_lens[b] are masked
+ * (probability exactly 0); a row with no valid key yields 0.
+ * dtype ZK_F16 (MFMA path) or ZK_F32 (fp32 path).
+ * Replaces zenith_cuda.flash_attention (cuda_bindings.cpp:90-106 ->
+ * flash_attention_forward core/src/flash_attention.cu:194-340) and its
+ * unbound FP16 twin (flash_attention.cu:55-188); mask rule from
+ * zenith/jax/primitives.py:302-310. */
+int zk_flash_attn_fwd(const void *Q, const void *K, const void *V, void *O,
+                      int64_t batch, int64_t heads, int64_t seq_q,
+                      int64_t seq_k, int64_t head_dim, const int64_t *strides,
+                      const int32_t *valid_lens, float scale, int dtype,
+                      void *stream);
+
+/* Symmetric int8 quantisation, q = clamp(round_half_even(x / scale),
+ * -128, 127), x in dtype ZK_F32 or ZK_F16 (n elements, contiguous).
+ * Replaces quantize_f32_to_int8_kernel (cuda_kernels.cu:918-937; numpy form
+ * benchmarks/int8_bench.py:19-27). */
+int zk_quantize_i8(const void *x, int8_t *q, int64_t n, float scale,
+                   int dtype, void *stream);
+
+/* INT8 GEMM on MFMA with int32 accumulation:
+ *   acc[M,N] = A_q[M,K] . W_q[N,K]^T   (both int8, K-major)
+ *   out_dtype ZK_I32: C = acc (raw accumulators; epilogue must be NONE)
+ *   out_dtype ZK_F16 / ZK_F32: C = epilogue(acc * (s_x * s_w[n]))
+ * s_w is fp32 [N] (per-output-channel weight scales), s_x the per-tensor
+ * activation scale; bias/residual in out_dtype.
+ * Replaces int8_matmul / fused_int8_linear (cuda_kernels.cu:963-1049;
+ * numpy form benchmarks/int8_bench.py:42-45). */
+int zk_gemm_i8(const int8_t *A, const int8_t *W, void *C, int64_t M,
+               int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc,
+               float s_x, const float *s_w, const void *bias,
+               const void *residual, int64_t ldr, int epilogue,
+               int out_dtype, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ZK_API_H */

@@ -1,0 +1,87 @@
+"""C-ABI checks that need no GPU: libzenith_hip.so loads, exports every
+function include/zk_api.h declares, and rejects bad arguments with the
+documented status codes before touching the device."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from zenith_amd import _lib as L
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    src = open(os.path.join(ROOT, "include", "zk_api.h")).read()
+    # function declarations: "<type> zk_name(" at the start of a line
+    return sorted(set(re.findall(r"^(?:const\s+)?\w+\s*\*?\s*(zk_[a-z0-9_]+)\s*\(", src, re.M)))
+
+
+def test_header_and_binding_agree():
+    assert _declared() == sorted(L.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = L.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.zk_version() >= 100
+
+
+@pytest.mark.parametrize("call,code", [
+    (lambda lib: lib.zk_relu(None, None, -1, L.ZK_F32, None), L.ZK_ERR_INVALID),
+    (lambda lib: lib.zk_relu(None, None, 5, L.ZK_F32, None), L.ZK_ERR_INVALID),
+    (lambda lib: lib.zk_relu(1, 1, 5, 7, None), L.ZK_ERR_UNSUPPORTED),
+    (lambda lib: lib.zk_gelu(1, None, 1, 2, 2, 9, L.ZK_F32, None), L.ZK_ERR_INVALID),
+    (lambda lib: lib.zk_layernorm(1, None, 1, 1, 1, 4, 0, 1e-5, L.ZK_F32, None), L.ZK_ERR_INVALID),
+    (lambda lib: lib.zk_layernorm(1, None, 1, 1, 1, 4, 8, -1.0, L.ZK_F32, None), L.ZK_ERR_INVALID),
+    (lambda lib: lib.zk_gemm_f16(16, 16, 16, 8, 8, 8, 8, 8, 8, 0, L.ZK_F16, None, None, 0, 0, None),
+     L.ZK_ERR_UNSUPPORTED),
+    (lambda lib: lib.zk_gemm_f16(16, 16, 16, 8, 8, 12, 12, 12, 8, 1, L.ZK_F16, None, None, 0, 0, None),
+     L.ZK_ERR_UNSUPPORTED),  # K not a multiple of 8
+    (lambda lib: lib.zk_gemm_f16(16, 16, 16, 8, 8, 8, 4, 8, 8, 1, L.ZK_F16, None, None, 0, 0, None),
+     L.ZK_ERR_INVALID),  # lda < K
+    (lambda lib: lib.zk_gemm_f16(16, 16, 16, 8, 8, 8, 8, 8, 8, 1, L.ZK_F16, None, None, 0, 1, None),
+     L.ZK_ERR_INVALID),  # bias epilogue without bias
+    (lambda lib: lib.zk_gemm_i8(16, 16, 16, 8, 8, 16, 16, 16, 8, 1.0, None, None, None, 0, 1,
+                                L.ZK_I32, None), L.ZK_ERR_INVALID),  # int32 out + epilogue
+    (lambda lib: lib.zk_gemm_i8(16, 16, 16, 8, 8, 16, 16, 16, 8, 1.0, None, None, None, 0, 0,
+                                L.ZK_F16, None), L.ZK_ERR_INVALID),  # dequant without s_w
+    (lambda lib: lib.zk_flash_attn_fwd(16, 16, 16, 16, 1, 1, 8, 8, 48, L.strides_arg([0] * 12),
+                                       None, 0.125, L.ZK_F16, None), L.ZK_ERR_UNSUPPORTED),
+    (lambda lib: lib.zk_flash_attn_fwd(16, 16, 16, 16, 1, 1, 8, 8, 64, L.strides_arg([0] * 12),
+                                       None, -1.0, L.ZK_F16, None), L.ZK_ERR_INVALID),
+    (lambda lib: lib.zk_quantize_i8(16, 16, 4, 0.0, L.ZK_F32, None), L.ZK_ERR_INVALID),
+    (lambda lib: lib.zk_transpose_f16(16, 16, 4, 8, 4, 4, None), L.ZK_ERR_INVALID),
+])
+def test_argument_errors(call, code):
+    lib = L.load()
+    assert call(lib) == code
+    assert L.last_error()
+
+
+def test_zero_sized_calls_are_noops():
+    lib = L.load()
+    assert lib.zk_relu(None, None, 0, L.ZK_F32, None) == L.ZK_OK
+    assert lib.zk_gemm_f16(None, None, None, 0, 8, 8, 8, 8, 8, 1, L.ZK_F16, None, None, 0, 0, None) == L.ZK_OK
+    assert lib.zk_layernorm(None, None, None, None, None, 0, 768, 1e-5, L.ZK_F16, None) == L.ZK_OK
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(RuntimeError, match="not found"):
+        L.load(str(tmp_path / "nope.so"))
+
+
+def test_call_raises_with_message():
+    with pytest.raises(RuntimeError, match="zk_relu"):
+        L.call("zk_relu", None, None, -1, L.ZK_F32, None)
+
+
+def test_c_types_are_plain():
+    # no torch / C++ types in the ABI: every argument is a pointer or scalar
+    for name, args in L.SIGNATURES.items():
+        for a in args:
+            assert a in (ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float) or \
+                a is ctypes.POINTER(ctypes.c_int64), (name, a)

@@ -1,0 +1,127 @@
+"""GPU parity: flash-attention forward (fp16 MFMA and fp32 paths) with the
+key-padding mask, vs the float64 dense masked-softmax oracle.
+
+fp16 bar: |O - ref| <= 2e-3 + 1e-2 |ref|; fp32 bar: 1e-5 abs + 1e-4 rel.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ops
+from tests.conftest import fp16_tol
+from zenith_amd import synthetic
+
+pytestmark = pytest.mark.gpu
+
+
+def _qkv(B, H, Sq, Sk, D, f16=True, tag=0):
+    q = synthetic.normal((B, H, Sq, D), tag=tag + 1)
+    k = synthetic.normal((B, H, Sk, D), tag=tag + 2)
+    v = synthetic.normal((B, H, Sk, D), tag=tag + 3)
+    if f16:
+        q, k, v = (synthetic.round_f16(a) for a in (q, k, v))
+    return q, k, v
+
+
+def _run(dev, q, k, v, lens, dtype):
+    from zenith_amd import zenith_cuda as zc
+
+    t = [torch.from_numpy(a).to(dev, dtype) for a in (q, k, v)]
+    tl = None if lens is None else torch.from_numpy(np.asarray(lens, np.int32)).to(dev)
+    return zc.flash_attention(*t, key_padding_lengths=tl).float().cpu().numpy()
+
+
+@pytest.mark.parametrize("B,H,S,D", [(2, 12, 128, 64), (2, 3, 512, 64), (3, 2, 77, 64),
+                                     (2, 2, 130, 128), (2, 2, 64, 32), (1, 1, 1, 64)])
+@pytest.mark.parametrize("masked", [False, True])
+def test_flash_attention_f16(dev, B, H, S, D, masked):
+    q, k, v = _qkv(B, H, S, S, D)
+    lens = None
+    if masked:
+        lens = np.random.default_rng(3).integers(S // 2, S, size=B, endpoint=True)
+        lens[0] = max(1, S // 2)
+    o = _run(dev, q, k, v, lens, torch.float16)
+    ok, worst = fp16_tol(o, ops.attention(q, k, v, lens))
+    assert ok, worst
+
+
+@pytest.mark.parametrize("S", [128, 512])
+def test_flash_attention_config3(dev, S):
+    """Config 3: B=32, H=12, D=64, lengths ~ U{S/2..S}; checked on 4 sequences
+    (batch entries are independent)."""
+    B, H, D = 32, 12, 64
+    q, k, v = _qkv(B, H, S, S, D, tag=10)
+    lens = synthetic.padding_lengths(B, S)
+    o = _run(dev, q, k, v, lens, torch.float16)
+    pick = [0, 7, 19, 31]
+    ok, worst = fp16_tol(o[pick], ops.attention(q[pick], k[pick], v[pick], lens[pick]))
+    assert ok, worst
+
+
+def test_flash_attention_edge_lengths(dev):
+    """Length 0 -> zero output; length 1 -> O = V[0]; length S -> unmasked."""
+    B, H, S, D = 4, 2, 96, 64
+    q, k, v = _qkv(B, H, S, S, D, tag=20)
+    lens = np.array([0, 1, S, 65], np.int32)
+    o = _run(dev, q, k, v, lens, torch.float16)
+    assert np.all(o[0] == 0)
+    np.testing.assert_allclose(o[1], np.broadcast_to(v[1, :, :1, :], o[1].shape), atol=2e-3, rtol=1e-2)
+    ok, worst = fp16_tol(o, ops.attention(q, k, v, lens))
+    assert ok, worst
+
+
+def test_flash_attention_uniform_keys(dev):
+    """Identical keys -> O = mean of the valid V rows (closed form)."""
+    B, H, S, D = 2, 2, 128, 64
+    q, _, v = _qkv(B, H, S, S, D, tag=30)
+    k = np.broadcast_to(synthetic.round_f16(synthetic.normal((1, 1, 1, D), tag=33)), (B, H, S, D)).copy()
+    lens = np.array([100, 37], np.int32)
+    o = _run(dev, q, k, v, lens, torch.float16)
+    for b in range(B):
+        mean = v[b, :, : lens[b], :].astype(np.float64).mean(axis=1, keepdims=True)
+        np.testing.assert_allclose(o[b], np.broadcast_to(mean, o[b].shape), atol=2e-3, rtol=1e-2)
+
+
+def test_flash_attention_strided_qkv(dev):
+    """Q/K/V read by stride out of a packed [B*S, 3H] projection, O written
+    into [B*S, H]: the layout the encoder uses (no transposes)."""
+    from zenith_amd import _lib as L
+
+    B, S, nh, D = 3, 128, 12, 64
+    H = nh * D
+    qkv = synthetic.round_f16(synthetic.normal((B * S, 3 * H), tag=40))
+    lens = np.array([128, 70, 64], np.int32)
+    tq = torch.from_numpy(qkv).to(dev, torch.float16)
+    out = torch.empty((B * S, H), dtype=torch.float16, device=dev)
+    base, es = tq.data_ptr(), 2
+    ld = 3 * H
+    L.call("zk_flash_attn_fwd", base, base + H * es, base + 2 * H * es, out.data_ptr(), B, nh, S, S, D,
+           L.strides_arg([S * ld, D, ld] * 3 + [S * H, D, H]),
+           torch.from_numpy(lens).to(dev).data_ptr(), 1.0 / math.sqrt(D), L.ZK_F16,
+           torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    x = qkv.reshape(B, S, 3, nh, D).transpose(2, 0, 3, 1, 4)  # 3,B,nh,S,D
+    ref = ops.attention(x[0], x[1], x[2], lens).transpose(0, 2, 1, 3).reshape(B * S, H)
+    ok, worst = fp16_tol(out.float().cpu().numpy(), ref)
+    assert ok, worst
+
+
+@pytest.mark.parametrize("B,H,S,D", [(2, 4, 128, 64), (1, 2, 77, 32), (2, 2, 65, 128)])
+@pytest.mark.parametrize("masked", [False, True])
+def test_flash_attention_f32(dev, B, H, S, D, masked):
+    q, k, v = _qkv(B, H, S, S, D, f16=False, tag=50)
+    lens = np.array([S // 2 + 1] + [S] * (B - 1), np.int32) if masked else None
+    o = _run(dev, q, k, v, lens, torch.float32)
+    np.testing.assert_allclose(o, ops.attention(q, k, v, lens), rtol=1e-4, atol=1e-5)
+
+
+def test_flash_attention_cross_lengths(dev):
+    """Sq != Sk."""
+    q, _, _ = _qkv(2, 2, 40, 40, 64, tag=60)
+    _, k, v = _qkv(2, 2, 200, 200, 64, tag=70)
+    o = _run(dev, q, k, v, [150, 200], torch.float16)
+    ok, worst = fp16_tol(o, ops.attention(q, k, v, np.array([150, 200])))
+    assert ok, worst

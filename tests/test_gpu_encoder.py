@@ -1,0 +1,116 @@
+"""GPU parity: BERT encoder (configs 1 and 5) through the fused HIP path vs
+the oracle's fp32 encoder on the same fp16-rounded weights and inputs.
+Bar: norm-relative error <= 2e-2 and |y - ref| <= 2e-2 + 2e-2 |ref|."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bert as obert
+from oracle import ops
+from zenith_amd import synthetic
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(y, ref, bar=2e-2):
+    rel = float(np.linalg.norm(y - ref) / np.linalg.norm(ref))
+    worst = float(np.max(np.abs(y - ref) - (bar + bar * np.abs(ref))))
+    assert rel <= bar and worst <= 0, (rel, worst)
+    return rel
+
+
+def _r16(layers):
+    return [{k: synthetic.round_f16(v) for k, v in w.items()} for w in layers]
+
+
+def test_config1_single_layer(dev):
+    from zenith_amd.encoder import BertEncoder
+
+    w = _r16(synthetic.bert_weights(1, seed=42))
+    x = synthetic.round_f16(synthetic.hidden_states(1, 128, seed=42))
+    enc = BertEncoder(w, device=dev)
+    y = enc(torch.from_numpy(x).to(dev, torch.float16)).float().cpu().numpy()
+    _check(y, obert.bert_encoder(x, w))
+
+
+@pytest.mark.parametrize("S", [128, 512])
+def test_config5_encoder_fp16(dev, S):
+    """12 layers, B=32, lengths ~ U{S/2..S}; the oracle runs on 2 of the 32
+    sequences (sequences are independent through the encoder)."""
+    from zenith_amd.encoder import BertEncoder
+
+    B = 32
+    w = _r16(synthetic.bert_weights(12, seed=42))
+    x = synthetic.round_f16(synthetic.hidden_states(B, S, seed=42))
+    lens = synthetic.padding_lengths(B, S)
+    enc = BertEncoder(w, device=dev)
+    y = enc(torch.from_numpy(x).to(dev, torch.float16), torch.from_numpy(lens).to(dev)).float().cpu().numpy()
+    assert np.isfinite(y).all()
+    pick = [0, 17]
+    _check(y[pick], obert.bert_encoder(x[pick], w, lens[pick]))
+
+
+def test_config5_encoder_int8_ffn(dev):
+    """INT8-FFN variant at B=32 S=128: scales calibrated on the GPU fp16 run,
+    the oracle's INT8 encoder uses the same scales and weight quantisation."""
+    from zenith_amd.encoder import BertEncoder
+
+    B, S = 32, 128
+    w = _r16(synthetic.bert_weights(12, seed=42))
+    x = synthetic.round_f16(synthetic.hidden_states(B, S, seed=42))
+    lens = synthetic.padding_lengths(B, S)
+    pick = [3]
+    # calibration on the oracle's fp32 activations of the picked sequence
+    s_x, s_h = [], []
+    h = x[pick]
+    for lw in w:
+        B1, S1, H = h.shape
+        # re-run the attention half of the layer to get h1
+        hx = h.reshape(-1, H)
+        q, k, v = (ops.linear(hx, lw[a], lw[b]) for a, b in (("Wq", "bq"), ("Wk", "bk"), ("Wv", "bv")))
+        sp = lambda t: t.reshape(B1, S1, 12, 64).transpose(0, 2, 1, 3)  # noqa: E731
+        ctx = ops.attention(sp(q), sp(k), sp(v), lens[pick]).astype(np.float32).transpose(0, 2, 1, 3).reshape(-1, H)
+        h1 = ops.add_layernorm(ops.linear(ctx, lw["Wo"], lw["bo"]), hx, lw["ln1_g"], lw["ln1_b"], 1e-12)
+        u = obert.ffn_activations(h1, lw)
+        s_x.append(float(ops.absmax_scale(np.abs(h1).max())))
+        s_h.append(float(ops.absmax_scale(np.abs(u).max())))
+        h = obert.bert_layer(h, lw, lens[pick])
+    enc = BertEncoder(w, device=dev)
+    enc.enable_int8_ffn(s_x, s_h, layers_fp32=w)
+    y = enc(torch.from_numpy(x).to(dev, torch.float16), torch.from_numpy(lens).to(dev)).float().cpu().numpy()
+    int8_layers = []
+    for i, lw in enumerate(w):
+        qi, si = ops.quantize_weight_per_channel(lw["Wi"])
+        qo, so = ops.quantize_weight_per_channel(lw["Wo2"])
+        # the encoder's torch-side weight quantiser must agree bit-for-bit
+        np.testing.assert_array_equal(enc.int8[i]["Wi_q"].cpu().numpy(), qi)
+        int8_layers.append({"Wi_q": qi, "s_wi": si, "Wo2_q": qo, "s_wo2": so,
+                            "s_x": np.float32(s_x[i]), "s_h": np.float32(s_h[i])})
+    ref = obert.bert_encoder(x[pick], w, lens[pick], int8_layers=int8_layers)
+    _check(y[pick], ref)
+    # and it stays close to the fp16 model
+    ref16 = obert.bert_encoder(x[pick], w, lens[pick])
+    assert np.linalg.norm(y[pick] - ref16) / np.linalg.norm(ref16) < 0.1
+
+
+def test_graph_replay_matches_eager(dev):
+    """HIP-graph replays (several, with eager work in between) reproduce the
+    eager forward bit-for-bit."""
+    from zenith_amd.encoder import BertEncoder
+
+    B, S = 8, 128
+    w = _r16(synthetic.bert_weights(2, seed=7))
+    x = torch.from_numpy(synthetic.round_f16(synthetic.hidden_states(B, S, seed=7))).to(dev, torch.float16)
+    lens = torch.from_numpy(synthetic.padding_lengths(B, S, seed=7)).to(dev)
+    enc = BertEncoder(w, device=dev)
+    eager = enc(x, lens).clone()
+    gx, gl, go = enc.capture(B, S)
+    for i in range(3):
+        gx.copy_(x)
+        gl.copy_(lens)
+        enc.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(go, eager), f"replay {i} differs"
+        _ = enc(x * 0.5, lens)  # eager work between replays
+        torch.cuda.synchronize()

@@ -1,0 +1,120 @@
+"""GPU parity: FP16 MFMA GEMM (wmma_matmul / linear with fused epilogues) and
+the fp32 `matmul`, vs the CPU oracle.
+
+FP16 GEMM bar: |C - ref| <= 2e-3 + 1e-2 |ref| with ref the float64 product of
+the same fp16-rounded inputs (every product is exact in float64). Large
+squares are checked on a seeded sample of rows (rows are independent).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ops
+from tests.conftest import fp16_tol
+from zenith_amd import synthetic
+
+pytestmark = pytest.mark.gpu
+
+BERT = [(4096, 768, 2304), (4096, 768, 768), (4096, 768, 3072), (4096, 3072, 768)]
+
+
+def _t(a, dev, dtype):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev, dtype)
+
+
+@pytest.mark.parametrize("M,K,N", [(128, 64, 256), (64, 64, 64), (100, 70, 37), (1, 8, 1),
+                                   (257, 136, 129), (1024, 1024, 1024)] + BERT)
+@pytest.mark.parametrize("out", [torch.float32, torch.float16])
+def test_wmma_matmul(dev, M, K, N, out):
+    from zenith_amd import zenith_cuda as zc
+
+    a = synthetic.round_f16(synthetic.uniform((M, K), tag=1))
+    b = synthetic.round_f16(synthetic.uniform((K, N), tag=2))
+    c = zc.wmma_matmul(_t(a, dev, torch.float16), _t(b, dev, torch.float16), out_dtype=out)
+    assert c.dtype == out and c.shape == (M, N)
+    ref = ops.matmul_f64(a, b)
+    ok, worst = fp16_tol(c.float().cpu().numpy(), ref)
+    assert ok, worst
+
+
+@pytest.mark.parametrize("n", [4096, 8192])
+def test_wmma_matmul_square_sampled(dev, n):
+    from zenith_amd import zenith_cuda as zc
+
+    a = synthetic.round_f16(synthetic.uniform((n, n), tag=3))
+    b = synthetic.round_f16(synthetic.uniform((n, n), tag=4))
+    c = zc.wmma_matmul(_t(a, dev, torch.float16), _t(b, dev, torch.float16), out_dtype=torch.float16)
+    rows = np.random.default_rng(7).choice(n, 48, replace=False)
+    ref = ops.matmul_f64(a[rows], b)
+    ok, worst = fp16_tol(c[torch.from_numpy(rows).to(dev)].float().cpu().numpy(), ref)
+    assert ok, worst
+
+
+def test_wmma_matmul_reference_kat(dev):
+    """[[1,2,3],[4,5,6]] . [[1,2],[3,4],[5,6]] = [[22,28],[49,64]]
+    (tests/test_kernels.cpp:68-86)."""
+    from zenith_amd import zenith_cuda as zc
+
+    a = torch.tensor([[1, 2, 3], [4, 5, 6]], dtype=torch.float16, device=dev)
+    b = torch.tensor([[1, 2], [3, 4], [5, 6]], dtype=torch.float16, device=dev)
+    np.testing.assert_array_equal(zc.wmma_matmul(a, b).cpu().numpy(), [[22, 28], [49, 64]])
+    np.testing.assert_array_equal(zc.matmul(a.float(), b.float()).cpu().numpy(), [[22, 28], [49, 64]])
+
+
+@pytest.mark.parametrize("act", [None, "gelu", "gelu_tanh", "relu", "residual"])
+@pytest.mark.parametrize("M,K,N", [(4096, 768, 3072), (4096, 3072, 768), (300, 768, 2304), (5, 24, 40)])
+def test_linear_epilogues(dev, act, M, K, N):
+    from zenith_amd import zenith_cuda as zc
+
+    x = synthetic.round_f16(synthetic.normal((M, K), tag=5))
+    w = synthetic.round_f16(synthetic.normal((N, K), tag=6, std=0.02))
+    b = synthetic.round_f16(synthetic.normal((N,), tag=7, std=0.5))
+    r = synthetic.round_f16(synthetic.normal((M, N), tag=8))
+    y = zc.linear(_t(x, dev, torch.float16), _t(w, dev, torch.float16), _t(b, dev, torch.float16),
+                  activation=None if act == "residual" else act,
+                  residual=_t(r, dev, torch.float16) if act == "residual" else None)
+    ref = ops.matmul_f64(x, w.T) + b
+    if act == "gelu":
+        ref = ops.gelu_erf(ref.astype(np.float32))
+    elif act == "gelu_tanh":
+        ref = ops.gelu_tanh(ref.astype(np.float32))
+    elif act == "relu":
+        ref = np.maximum(ref, 0)
+    elif act == "residual":
+        ref = ref + r
+    ok, worst = fp16_tol(y.float().cpu().numpy(), ref)
+    assert ok, worst
+
+
+def test_linear_3d_and_no_bias(dev):
+    from zenith_amd import zenith_cuda as zc
+
+    x = synthetic.round_f16(synthetic.normal((4, 33, 768), tag=9))
+    w = synthetic.round_f16(synthetic.normal((768, 768), tag=10, std=0.02))
+    y = zc.linear(_t(x, dev, torch.float16), _t(w, dev, torch.float16))
+    assert y.shape == (4, 33, 768)
+    ok, worst = fp16_tol(y.float().cpu().numpy(), ops.matmul_f64(x, w.T))
+    assert ok, worst
+
+
+@pytest.mark.parametrize("M,K,N", [(2, 3, 2), (128, 768, 768), (100, 70, 37), (513, 1000, 65)])
+def test_matmul_fp32(dev, M, K, N):
+    from zenith_amd import zenith_cuda as zc
+
+    a = synthetic.uniform((M, K), tag=11)
+    b = synthetic.uniform((K, N), tag=12)
+    c = zc.matmul(_t(a, dev, torch.float32), _t(b, dev, torch.float32))
+    assert c.dtype == torch.float32
+    np.testing.assert_allclose(c.cpu().numpy(), ops.matmul_f64(a, b), rtol=1e-5, atol=1e-4)
+
+
+def test_linear_fp32(dev):
+    from zenith_amd import zenith_cuda as zc
+
+    x = synthetic.normal((64, 768), tag=13)
+    w = synthetic.normal((3072, 768), tag=14, std=0.02)
+    b = synthetic.normal((3072,), tag=15)
+    y = zc.linear(_t(x, dev, torch.float32), _t(w, dev, torch.float32), _t(b, dev, torch.float32),
+                  activation="gelu")
+    np.testing.assert_allclose(y.cpu().numpy(), ops.gelu_erf(ops.linear(x, w, b)), rtol=1e-4, atol=1e-5)

@@ -1,0 +1,125 @@
+"""GPU parity: LayerNorm / Add+LayerNorm, GELU / bias+GELU, ReLU, int8
+quantisation — HIP kernels through the C ABI vs the CPU oracle.
+
+Tolerances: fp32 I/O 1e-5 abs + 1e-5 rel (reference bar for LN is rtol 1e-4 /
+atol 1e-5, tests/test_layernorm_parallel.py:45-79); fp16 outputs
+|y - ref| <= 2e-3 + 1e-2 |ref| (north-star fp16 bar); quantisation bit-exact.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ops
+from tests.conftest import fp16_tol
+from zenith_amd import synthetic
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev, dtype):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev, dtype)
+
+
+@pytest.mark.parametrize("rows,hidden", [(1, 768), (128, 768), (4096, 768), (33, 1024),
+                                         (7, 100), (5, 3), (16, 8192), (3, 20000)])
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("with_res", [False, True])
+def test_layernorm(dev, rows, hidden, dtype, with_res):
+    from zenith_amd import zenith_cuda as zc
+
+    x = synthetic.normal((rows, hidden), tag=1) * 3 + 0.5
+    r = synthetic.normal((rows, hidden), tag=2)
+    g = synthetic.normal((hidden,), tag=3, std=0.5) + 1
+    b = synthetic.normal((hidden,), tag=4, std=0.1)
+    eps = 1e-12 if hidden == 768 else 1e-5
+    tdt = torch.float32 if dtype == "f32" else torch.float16
+    if dtype == "f16":
+        x, r, g, b = (synthetic.round_f16(a) for a in (x, r, g, b))
+    if with_res:
+        y = zc.add_layernorm(_t(x, dev, tdt), _t(r, dev, tdt), _t(g, dev, tdt), _t(b, dev, tdt), eps)
+        ref = ops.add_layernorm(x, r, g, b, eps)
+    else:
+        y = zc.layernorm(_t(x, dev, tdt), _t(g, dev, tdt), _t(b, dev, tdt), eps)
+        ref = ops.layernorm(x, g, b, eps)
+    y = y.float().cpu().numpy()
+    if dtype == "f32":
+        np.testing.assert_allclose(y, ref, rtol=1e-5, atol=1e-5)
+    else:
+        ok, worst = fp16_tol(y, ref)
+        assert ok, worst
+
+
+def test_layernorm_default_eps_and_unit_stats(dev):
+    """layernorm(input, gamma, beta) uses eps=1e-5 like the reference
+    binding; with gamma=1, beta=0 rows have mean 0 / std 1."""
+    from zenith_amd import zenith_cuda as zc
+
+    x = synthetic.normal((64, 768), tag=9) * 4 + 2
+    y = zc.layernorm(_t(x, dev, torch.float32), torch.ones(768, device=dev),
+                     torch.zeros(768, device=dev)).cpu().numpy()
+    np.testing.assert_allclose(y, ops.layernorm(x, np.ones(768, np.float32),
+                                                np.zeros(768, np.float32), 1e-5), rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(y.mean(-1), 0, atol=1e-5)
+    np.testing.assert_allclose(y.std(-1), 1, atol=1e-4)
+
+
+@pytest.mark.parametrize("shape", [(4096, 3072), (3, 5), (1000,), (128, 768), (17, 24)])
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("mode", ["tanh", "none"])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_gelu(dev, shape, dtype, mode, with_bias):
+    from zenith_amd import zenith_cuda as zc
+
+    x = synthetic.normal(shape, tag=5) * 3
+    bias = synthetic.normal((shape[-1],), tag=6) if with_bias else None
+    tdt = torch.float32 if dtype == "f32" else torch.float16
+    if dtype == "f16":
+        x = synthetic.round_f16(x)
+        bias = None if bias is None else synthetic.round_f16(bias)
+    tb = None if bias is None else _t(bias, dev, tdt)
+    y = zc.bias_gelu(_t(x, dev, tdt), tb, approximate=mode).float().cpu().numpy()
+    ref = ops.bias_gelu(x, bias, "tanh" if mode == "tanh" else "erf")
+    if dtype == "f32":
+        np.testing.assert_allclose(y, ref, rtol=1e-5, atol=1e-6)
+    else:
+        ok, worst = fp16_tol(y, ref)
+        assert ok, worst
+
+
+def test_gelu_reference_kats(dev):
+    """GELU(1) ~ 0.841, GELU(0) = 0, GELU(-1) ~ -0.159 (+-0.01), the reference's
+    known answers (tests/test_cuda_cublas_bindings.py:36-57)."""
+    from zenith_amd import zenith_cuda as zc
+
+    y = zc.gelu(torch.tensor([1.0, 0.0, -1.0], device=dev)).cpu().numpy()
+    assert abs(y[0] - 0.841) < 0.01 and y[1] == 0.0 and abs(y[2] + 0.159) < 0.01
+
+
+@pytest.mark.parametrize("n", [1, 7, 4096 * 768 + 5])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_relu(dev, n, dtype):
+    from zenith_amd import zenith_cuda as zc
+
+    x = synthetic.normal((n,), tag=7)
+    y = zc.relu(_t(x, dev, dtype)).float().cpu().numpy()
+    np.testing.assert_array_equal(y, ops.relu(x.astype(np.float16 if dtype == torch.float16 else np.float32)).astype(np.float32))
+
+
+@pytest.mark.parametrize("n", [1, 9, 4096 * 768, 4096 * 3072 + 3])
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_quantize_bit_exact(dev, n, dtype):
+    from zenith_amd import zenith_cuda as zc
+
+    x = synthetic.normal((n,), tag=8) * 2
+    if dtype == "f16":
+        x = synthetic.round_f16(x)
+    # ties: exact multiples of scale/2 must round half to even
+    s = np.float32(0.0625)
+    x[: min(n, 6)] = np.array([0.03125, 0.09375, -0.03125, -0.09375, 100.0, -100.0], np.float32)[: min(n, 6)]
+    tdt = torch.float32 if dtype == "f32" else torch.float16
+    q = zc.quantize_int8(_t(x, dev, tdt), float(s)).cpu().numpy()
+    np.testing.assert_array_equal(q, ops.quantize_int8(x, s))
+    s2 = ops.absmax_scale(np.abs(x).max())
+    q2 = zc.quantize_int8(_t(x, dev, tdt), float(s2)).cpu().numpy()
+    np.testing.assert_array_equal(q2, ops.quantize_int8(x, s2))

@@ -1,0 +1,318 @@
+// Flash-attention forward (non-causal, optional key-padding mask).
+//
+// fp16 path (MFMA). A workgroup of NW wavefronts owns NW*32 query rows of
+// one (batch, head); every wavefront owns 32 of them. Keys are walked in
+// tiles of 64: K is staged in LDS as [key][d] and V transposed as [d][key].
+// The wavefront computes S^T = K . Q^T with 32x32x16 MFMAs, so each lane
+// ends up holding 32 keys of ONE query column (lane % 32): the row max and
+// row sum of the online softmax are then a register loop plus a single
+// swap with lane ^ 32, and the per-query rescale factor is lane-uniform.
+// The exponentiated scores, rounded to fp16, are already laid out as the B
+// operand of O^T += V^T . P^T, so P never leaves registers. Statistics and
+// accumulation are fp32; exp2 with the softmax scale folded into log2(e).
+// Key tiles at or beyond the sequence's valid length are never loaded; keys
+// >= valid length inside the last tile get probability exactly 0, and a
+// query with no valid key produces 0 (mask rule of the reference's masked
+// attention primitive).
+//
+// fp32 path (SIMT): D/32 lanes per query, each holding 32 dims of q and of
+// the output accumulator; K/V tiles in LDS are read as broadcasts.
+#include "zk_common.hpp"
+
+namespace zk {
+
+struct AttnParams {
+  const void *Q, *K, *V;
+  void *O;
+  int B, H, Sq, Sk;
+  int64_t sq[3], sk[3], sv[3], so[3];  // (batch, head, seq) strides
+  const int32_t *valid_lens;
+  float scale_log2;  // softmax scale * log2(e)
+};
+
+__device__ __forceinline__ int valid_len(const AttnParams &p, int b) {
+  if (!p.valid_lens) return p.Sk;
+  int L = p.valid_lens[b];
+  return L < 0 ? 0 : (L > p.Sk ? p.Sk : L);
+}
+
+template <int D, int NW>
+__global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
+  constexpr int KT = 64;
+  constexpr int NT = NW * 64;
+  constexpr int KLD = D + 8;   // K tile row pitch (halves)
+  constexpr int VLD = KT + 4;  // V^T tile row pitch (halves)
+  constexpr int DV = D / 8;    // 16-byte vectors per K/V row
+  constexpr int PER = KT * DV / NT;
+  static_assert(KT * DV % NT == 0, "tile/thread mismatch");
+  __shared__ __attribute__((aligned(16))) f16 Ks[KT * KLD];
+  __shared__ __attribute__((aligned(16))) f16 Vt[D * VLD];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h32 = lane >> 5;
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int L = valid_len(p, b);
+  const f16 *Qb = (const f16 *)p.Q + b * p.sq[0] + h * p.sq[1];
+  const f16 *Kb = (const f16 *)p.K + b * p.sk[0] + h * p.sk[1];
+  const f16 *Vb = (const f16 *)p.V + b * p.sv[0] + h * p.sv[1];
+  f16 *Ob = (f16 *)p.O + b * p.so[0] + h * p.so[1];
+
+  const int qrow = blockIdx.x * (NW * 32) + wave * 32 + (lane & 31);
+  const bool qvalid = qrow < p.Sq;
+  f16x8 qf[D / 16];
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c)
+    qf[c] = qvalid ? *(const f16x8 *)(Qb + qrow * p.sq[2] + c * 16 + h32 * 8)
+                   : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+
+  f32x16 o[D / 32];
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
+  float m = -__builtin_inff(), l = 0.f;
+
+  const int ntiles = (L + KT - 1) / KT;
+  f16x8 kr[PER], vr[PER];
+  auto load_kv = [&](int t) {
+#pragma unroll
+    for (int v = 0; v < PER; ++v) {
+      const int idx = tid + v * NT;
+      const int kk = t * KT + idx / DV;  // K: 16-byte vectors row-contiguous
+      kr[v] = kk < p.Sk ? *(const f16x8 *)(Kb + kk * p.sk[2] + (idx % DV) * 8)
+                        : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      const int kv = t * KT + idx % KT;  // V: one key per lane (transposed store)
+      vr[v] = kv < p.Sk ? *(const f16x8 *)(Vb + kv * p.sv[2] + (idx / KT) * 8)
+                        : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  };
+  auto stash_kv = [&]() {
+#pragma unroll
+    for (int v = 0; v < PER; ++v) {
+      const int idx = tid + v * NT;
+      *(f16x8 *)(Ks + (idx / DV) * KLD + (idx % DV) * 8) = kr[v];
+      const int key = idx % KT, d0 = (idx / KT) * 8;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) Vt[(d0 + j) * VLD + key] = vr[v][j];
+    }
+  };
+
+  if (ntiles > 0) load_kv(0);
+  for (int t = 0; t < ntiles; ++t) {
+    __syncthreads();  // every wavefront is done with the previous tile
+    stash_kv();
+    __syncthreads();
+    if (t + 1 < ntiles) load_kv(t + 1);
+
+    // S^T[key][q] for the tile's two 32-key blocks.
+    f32x16 s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) {
+        const f16x8 kf = *(const f16x8 *)(Ks + (kb * 32 + (lane & 31)) * KLD + c * 16 + h32 * 8);
+        s[kb] = mfma32x32x16(kf, qf[c], s[kb]);
+      }
+    }
+    // Scale into the log2 domain, mask, tile max.
+    float tmax = -__builtin_inff();
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = t * KT + kb * 32 + 8 * (r >> 2) + 4 * h32 + (r & 3);
+        const float v = key < L ? s[kb][r] * p.scale_log2 : -__builtin_inff();
+        s[kb][r] = v;
+        tmax = fmaxf(tmax, v);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m, tmax);  // finite: key t*KT < L is valid
+    const float alpha = exp2f(m - m_new);
+    m = m_new;
+    float psum = 0.f;
+    f16x8 pf[2][2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float e = exp2f(s[kb][r] - m);
+        psum += e;
+        pf[kb][r >> 3][r & 7] = (f16)e;
+      }
+    psum += __shfl_xor(psum, 32, 64);
+    l = l * alpha + psum;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+    // O^T[d][q] += V^T[d][key] . P^T[key][q], 16 keys per MFMA. Lane-half
+    // h32, slot j of the P^T fragment holds key 16*c2 + 8*(j/4) + 4*h32 +
+    // j%4 of block kb; the V^T fragment is read with the same key order.
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2) {
+          const f16 *vrow = Vt + (dt * 32 + (lane & 31)) * VLD + kb * 32 + c2 * 16 + 4 * h32;
+          const f16x4 lo = *(const f16x4 *)vrow;
+          const f16x4 hi = *(const f16x4 *)(vrow + 8);
+          const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          o[dt] = mfma32x32x16(vf, pf[kb][c2], o[dt]);
+        }
+  }
+
+  if (qvalid) {
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f16x4 out;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out[j] = (f16)(o[dt][4 * g + j] * inv);
+        *(f16x4 *)(Ob + qrow * p.so[2] + dt * 32 + 8 * g + 4 * h32) = out;
+      }
+  }
+}
+
+// ---------------------------------------------------------------- fp32 ----
+template <int D>
+__global__ __launch_bounds__(256) void fa_fwd_f32_kernel(AttnParams p) {
+  constexpr int TPQ = D / 32;  // lanes per query
+  constexpr int QPB = 256 / TPQ;
+  constexpr int KT = 32;
+  __shared__ float Ks[KT][D + 4];
+  __shared__ float Vs[KT][D + 4];
+  const int tid = threadIdx.x, part = tid % TPQ;
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int L = valid_len(p, b);
+  const float *Qb = (const float *)p.Q + b * p.sq[0] + h * p.sq[1];
+  const float *Kb = (const float *)p.K + b * p.sk[0] + h * p.sk[1];
+  const float *Vb = (const float *)p.V + b * p.sv[0] + h * p.sv[1];
+  float *Ob = (float *)p.O + b * p.so[0] + h * p.so[1];
+  const int qrow = blockIdx.x * QPB + tid / TPQ;
+  const bool qvalid = qrow < p.Sq;
+  const float scale = p.scale_log2;
+
+  float q[32], acc[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    q[i] = qvalid ? Qb[qrow * p.sq[2] + part * 32 + i] : 0.f;
+    acc[i] = 0.f;
+  }
+  float m = -__builtin_inff(), l = 0.f;
+  const int ntiles = (L + KT - 1) / KT;
+  for (int t = 0; t < ntiles; ++t) {
+    __syncthreads();
+    for (int idx = tid; idx < KT * D; idx += 256) {
+      const int kk = idx / D, d = idx % D, key = t * KT + kk;
+      Ks[kk][d] = key < p.Sk ? Kb[key * p.sk[2] + d] : 0.f;
+      Vs[kk][d] = key < p.Sk ? Vb[key * p.sv[2] + d] : 0.f;
+    }
+    __syncthreads();
+    float s[KT];
+    float tmax = -__builtin_inff();
+#pragma unroll
+    for (int j = 0; j < KT; ++j) {
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) d = fmaf(q[i], Ks[j][part * 32 + i], d);
+#pragma unroll
+      for (int o = 1; o < TPQ; o <<= 1) d += __shfl_xor(d, o, 64);
+      s[j] = (t * KT + j < L) ? d * scale : -__builtin_inff();
+      tmax = fmaxf(tmax, s[j]);
+    }
+    const float m_new = fmaxf(m, tmax);
+    const float alpha = exp2f(m - m_new);
+    m = m_new;
+    l *= alpha;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) acc[i] *= alpha;
+#pragma unroll
+    for (int j = 0; j < KT; ++j) {
+      const float e = exp2f(s[j] - m);
+      l += e;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) acc[i] = fmaf(e, Vs[j][part * 32 + i], acc[i]);
+    }
+  }
+  if (qvalid) {
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) Ob[qrow * p.so[2] + part * 32 + i] = acc[i] * inv;
+  }
+}
+
+template <int D>
+static void launch_f16(const AttnParams &p, hipStream_t s) {
+  const int64_t blocks128 = (int64_t)p.B * p.H * ((p.Sq + 127) / 128);
+  if (blocks128 >= 1024) {
+    dim3 grid((unsigned)((p.Sq + 127) / 128), (unsigned)p.H, (unsigned)p.B);
+    fa_fwd_f16_kernel<D, 4><<<grid, 256, 0, s>>>(p);
+  } else {
+    dim3 grid((unsigned)((p.Sq + 63) / 64), (unsigned)p.H, (unsigned)p.B);
+    fa_fwd_f16_kernel<D, 2><<<grid, 128, 0, s>>>(p);
+  }
+}
+
+template <int D>
+static void launch_f32(const AttnParams &p, hipStream_t s) {
+  constexpr int QPB = 256 / (D / 32);
+  dim3 grid((unsigned)((p.Sq + QPB - 1) / QPB), (unsigned)p.H, (unsigned)p.B);
+  fa_fwd_f32_kernel<D><<<grid, 256, 0, s>>>(p);
+}
+
+}  // namespace zk
+
+using namespace zk;
+
+extern "C" int zk_flash_attn_fwd(const void *Q, const void *K, const void *V,
+                                 void *O, int64_t batch, int64_t heads,
+                                 int64_t seq_q, int64_t seq_k,
+                                 int64_t head_dim, const int64_t *strides,
+                                 const int32_t *valid_lens, float scale,
+                                 int dtype, void *stream) {
+  if (batch < 0 || heads < 0 || seq_q < 0 || seq_k < 0 || head_dim <= 0)
+    return fail(ZK_ERR_INVALID, "zk_flash_attn_fwd: bad size");
+  if (batch == 0 || heads == 0 || seq_q == 0) return ZK_OK;
+  if (!Q || !K || !V || !O || !strides)
+    return fail(ZK_ERR_INVALID, "zk_flash_attn_fwd: null pointer");
+  if (batch > 65535 || heads > 65535 || seq_q > 0x7fffffff || seq_k > 0x7fffffff)
+    return fail(ZK_ERR_UNSUPPORTED, "zk_flash_attn_fwd: size exceeds launch limits");
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128)
+    return fail(ZK_ERR_UNSUPPORTED, "zk_flash_attn_fwd: head_dim %lld not in {32, 64, 128}",
+                (long long)head_dim);
+  if (!(scale > 0.0f) || scale == __builtin_inff())
+    return fail(ZK_ERR_INVALID, "zk_flash_attn_fwd: scale must be finite and > 0");
+  for (int i = 0; i < 12; ++i)
+    if (strides[i] < 0) return fail(ZK_ERR_INVALID, "zk_flash_attn_fwd: negative stride");
+  AttnParams p;
+  p.Q = Q; p.K = K; p.V = V; p.O = O;
+  p.B = (int)batch; p.H = (int)heads; p.Sq = (int)seq_q; p.Sk = (int)seq_k;
+  for (int i = 0; i < 3; ++i) {
+    p.sq[i] = strides[i]; p.sk[i] = strides[3 + i];
+    p.sv[i] = strides[6 + i]; p.so[i] = strides[9 + i];
+  }
+  p.valid_lens = valid_lens;
+  p.scale_log2 = scale * 1.4426950408889634f;
+  hipStream_t s = as_stream(stream);
+  if (dtype == ZK_F16) {
+    for (int i = 0; i < 12; ++i)
+      if (strides[i] % 8)
+        return fail(ZK_ERR_UNSUPPORTED, "zk_flash_attn_fwd: fp16 strides must be multiples of 8");
+    if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O))
+      return fail(ZK_ERR_UNSUPPORTED, "zk_flash_attn_fwd: fp16 tensors must be 16-byte aligned");
+    if (head_dim == 32) launch_f16<32>(p, s);
+    else if (head_dim == 64) launch_f16<64>(p, s);
+    else launch_f16<128>(p, s);
+  } else if (dtype == ZK_F32) {
+    if (head_dim == 32) launch_f32<32>(p, s);
+    else if (head_dim == 64) launch_f32<64>(p, s);
+    else launch_f32<128>(p, s);
+  } else {
+    return fail(ZK_ERR_UNSUPPORTED, "zk_flash_attn_fwd: dtype %d not supported", dtype);
+  }
+  return check_launch("zk_flash_attn_fwd");
+}

@@ -1,0 +1,244 @@
+// Bandwidth-bound elementwise kernels: ReLU, (bias+)GELU, int8 quantisation
+// and the fp16 transpose. Every kernel moves 16-byte vectors per lane where
+// the shape and alignment allow it and falls back to a scalar grid-stride
+// loop otherwise.
+#include "zk_common.hpp"
+
+namespace zk {
+
+template <typename T> struct Vec16;
+template <> struct Vec16<f16> { typedef f16x8 type; static constexpr int n = 8; };
+template <> struct Vec16<float> { typedef f32x4 type; static constexpr int n = 4; };
+
+static inline int grid_for(int64_t work, int block) {
+  int64_t g = (work + block - 1) / block;
+  if (g > 65536) g = 65536;  // grid-stride loops cover the rest
+  if (g < 1) g = 1;
+  return (int)g;
+}
+
+// ------------------------------------------------------------------ ReLU --
+template <typename T>
+__global__ void relu_vec(const T *__restrict__ x, T *__restrict__ y,
+                         int64_t nvec) {
+  typedef typename Vec16<T>::type V;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nvec;
+       i += stride) {
+    V v = reinterpret_cast<const V *>(x)[i];
+#pragma unroll
+    for (int j = 0; j < Vec16<T>::n; ++j) v[j] = v[j] > (T)0 ? v[j] : (T)0;
+    reinterpret_cast<V *>(y)[i] = v;
+  }
+}
+
+template <typename T>
+__global__ void relu_scalar(const T *__restrict__ x, T *__restrict__ y,
+                            int64_t begin, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = begin + blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+       i < n; i += stride)
+    y[i] = x[i] > (T)0 ? x[i] : (T)0;
+}
+
+template <typename T>
+static int relu_impl(const void *xv, void *yv, int64_t n, hipStream_t s) {
+  const T *x = (const T *)xv;
+  T *y = (T *)yv;
+  constexpr int W = Vec16<T>::n;
+  int64_t nvec = (aligned16(x) && aligned16(y)) ? n / W : 0;
+  if (nvec > 0) relu_vec<T><<<grid_for(nvec, 256), 256, 0, s>>>(x, y, nvec);
+  if (nvec * W < n)
+    relu_scalar<T><<<grid_for(n - nvec * W, 256), 256, 0, s>>>(x, y, nvec * W, n);
+  return check_launch("zk_relu");
+}
+
+// ------------------------------------------------------------------ GELU --
+template <int MODE>
+__device__ __forceinline__ float gelu(float v) {
+  return MODE == ZK_GELU_ERF ? gelu_erf(v) : gelu_tanh(v);
+}
+
+// One 16-byte vector per iteration; requires cols % W == 0 so a vector never
+// straddles two rows and the bias slice is contiguous.
+template <typename T, int MODE, bool BIAS>
+__global__ void gelu_vec(const T *__restrict__ x, const T *__restrict__ bias,
+                         T *__restrict__ y, int64_t nvec, int64_t cols) {
+  typedef typename Vec16<T>::type V;
+  constexpr int W = Vec16<T>::n;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nvec;
+       i += stride) {
+    V v = reinterpret_cast<const V *>(x)[i];
+    V b;
+    if (BIAS) b = *reinterpret_cast<const V *>(bias + (i * W) % cols);
+    V o;
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+      float f = (float)v[j];
+      if (BIAS) f += (float)b[j];
+      o[j] = (T)gelu<MODE>(f);
+    }
+    reinterpret_cast<V *>(y)[i] = o;
+  }
+}
+
+template <typename T, int MODE, bool BIAS>
+__global__ void gelu_scalar(const T *__restrict__ x, const T *__restrict__ bias,
+                            T *__restrict__ y, int64_t n, int64_t cols) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += stride) {
+    float f = (float)x[i];
+    if (BIAS) f += (float)bias[i % cols];
+    y[i] = (T)gelu<MODE>(f);
+  }
+}
+
+template <typename T, int MODE, bool BIAS>
+static void gelu_launch(const T *x, const T *bias, T *y, int64_t n,
+                        int64_t cols, hipStream_t s) {
+  constexpr int W = Vec16<T>::n;
+  const bool vec = aligned16(x) && aligned16(y) && cols % W == 0 &&
+                   (!BIAS || aligned16(bias));
+  if (vec)
+    gelu_vec<T, MODE, BIAS><<<grid_for(n / W, 256), 256, 0, s>>>(x, bias, y, n / W, cols);
+  else
+    gelu_scalar<T, MODE, BIAS><<<grid_for(n, 256), 256, 0, s>>>(x, bias, y, n, cols);
+}
+
+template <typename T>
+static int gelu_impl(const void *x, const void *bias, void *y, int64_t n,
+                     int64_t cols, int mode, hipStream_t s) {
+  const T *xp = (const T *)x, *bp = (const T *)bias;
+  T *yp = (T *)y;
+  if (mode == ZK_GELU_ERF) {
+    if (bp) gelu_launch<T, ZK_GELU_ERF, true>(xp, bp, yp, n, cols, s);
+    else gelu_launch<T, ZK_GELU_ERF, false>(xp, bp, yp, n, cols, s);
+  } else {
+    if (bp) gelu_launch<T, ZK_GELU_TANH, true>(xp, bp, yp, n, cols, s);
+    else gelu_launch<T, ZK_GELU_TANH, false>(xp, bp, yp, n, cols, s);
+  }
+  return check_launch("zk_gelu");
+}
+
+// -------------------------------------------------------------- quantise --
+__device__ __forceinline__ int8_t quant1(float x, float scale) {
+  // IEEE division (hipcc keeps fp32 '/' correctly rounded), then
+  // round-half-to-even and saturate to the int8 range.
+  float r = __builtin_rintf(x / scale);
+  r = fminf(fmaxf(r, -128.0f), 127.0f);
+  return (int8_t)(int)r;
+}
+
+__global__ void quant_f16_vec(const f16 *__restrict__ x, int8_t *__restrict__ q,
+                              int64_t nvec, float scale) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nvec;
+       i += stride) {
+    f16x8 v = reinterpret_cast<const f16x8 *>(x)[i];
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      lo |= (uint32_t)(uint8_t)quant1((float)v[j], scale) << (8 * j);
+      hi |= (uint32_t)(uint8_t)quant1((float)v[j + 4], scale) << (8 * j);
+    }
+    reinterpret_cast<uint2 *>(q)[i] = make_uint2(lo, hi);
+  }
+}
+
+template <typename T>
+__global__ void quant_scalar(const T *__restrict__ x, int8_t *__restrict__ q,
+                             int64_t begin, int64_t n, float scale) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = begin + blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+       i < n; i += stride)
+    q[i] = quant1((float)x[i], scale);
+}
+
+// ------------------------------------------------------------- transpose --
+// 64x64 tile through LDS; scalar, bounds-checked accesses that are coalesced
+// along the fast axis on both sides.
+__global__ void transpose_f16_kernel(const f16 *__restrict__ src,
+                                     f16 *__restrict__ dst, int64_t rows,
+                                     int64_t cols, int64_t lds, int64_t ldd) {
+  __shared__ f16 tile[64][65];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t gr = r0 + r, gc = c0 + tx;
+    tile[r][tx] = (gr < rows && gc < cols) ? src[gr * lds + gc] : (f16)0;
+  }
+  __syncthreads();
+  for (int c = ty; c < 64; c += 4) {
+    const int64_t gc = c0 + c, gr = r0 + tx;  // dst row = source column
+    if (gc < cols && gr < rows) dst[gc * ldd + gr] = tile[tx][c];
+  }
+}
+
+}  // namespace zk
+
+using namespace zk;
+
+extern "C" int zk_relu(const void *x, void *y, int64_t n, int dtype,
+                       void *stream) {
+  if (n < 0) return fail(ZK_ERR_INVALID, "zk_relu: negative size");
+  if (n == 0) return ZK_OK;
+  if (!x || !y) return fail(ZK_ERR_INVALID, "zk_relu: null pointer");
+  if (dtype == ZK_F32) return relu_impl<float>(x, y, n, as_stream(stream));
+  if (dtype == ZK_F16) return relu_impl<f16>(x, y, n, as_stream(stream));
+  return fail(ZK_ERR_UNSUPPORTED, "zk_relu: dtype %d not supported", dtype);
+}
+
+extern "C" int zk_gelu(const void *x, const void *bias, void *y, int64_t rows,
+                       int64_t cols, int mode, int dtype, void *stream) {
+  if (rows < 0 || cols < 0) return fail(ZK_ERR_INVALID, "zk_gelu: negative size");
+  if (rows == 0 || cols == 0) return ZK_OK;
+  if (!x || !y) return fail(ZK_ERR_INVALID, "zk_gelu: null pointer");
+  if (mode != ZK_GELU_TANH && mode != ZK_GELU_ERF)
+    return fail(ZK_ERR_INVALID, "zk_gelu: bad mode %d", mode);
+  const int64_t n = rows * cols;
+  if (dtype == ZK_F32) return gelu_impl<float>(x, bias, y, n, cols, mode, as_stream(stream));
+  if (dtype == ZK_F16) return gelu_impl<f16>(x, bias, y, n, cols, mode, as_stream(stream));
+  return fail(ZK_ERR_UNSUPPORTED, "zk_gelu: dtype %d not supported", dtype);
+}
+
+extern "C" int zk_quantize_i8(const void *x, int8_t *q, int64_t n, float scale,
+                              int dtype, void *stream) {
+  if (n < 0) return fail(ZK_ERR_INVALID, "zk_quantize_i8: negative size");
+  if (n == 0) return ZK_OK;
+  if (!x || !q) return fail(ZK_ERR_INVALID, "zk_quantize_i8: null pointer");
+  if (!(scale > 0.0f) || scale != scale || scale == __builtin_inff())
+    return fail(ZK_ERR_INVALID, "zk_quantize_i8: scale must be finite and > 0");
+  hipStream_t s = as_stream(stream);
+  if (dtype == ZK_F16) {
+    const int64_t nvec =
+        (aligned16(x) && (reinterpret_cast<uintptr_t>(q) & 7u) == 0) ? n / 8 : 0;
+    if (nvec > 0)
+      quant_f16_vec<<<grid_for(nvec, 256), 256, 0, s>>>((const f16 *)x, q, nvec, scale);
+    if (nvec * 8 < n)
+      quant_scalar<f16><<<grid_for(n - nvec * 8, 256), 256, 0, s>>>(
+          (const f16 *)x, q, nvec * 8, n, scale);
+  } else if (dtype == ZK_F32) {
+    quant_scalar<float><<<grid_for(n, 256), 256, 0, s>>>((const float *)x, q, 0, n, scale);
+  } else {
+    return fail(ZK_ERR_UNSUPPORTED, "zk_quantize_i8: dtype %d not supported", dtype);
+  }
+  return check_launch("zk_quantize_i8");
+}
+
+extern "C" int zk_transpose_f16(const void *src, void *dst, int64_t rows,
+                                int64_t cols, int64_t lds, int64_t ldd,
+                                void *stream) {
+  if (rows < 0 || cols < 0) return fail(ZK_ERR_INVALID, "zk_transpose_f16: negative size");
+  if (rows == 0 || cols == 0) return ZK_OK;
+  if (!src || !dst) return fail(ZK_ERR_INVALID, "zk_transpose_f16: null pointer");
+  if (lds < cols || ldd < rows)
+    return fail(ZK_ERR_INVALID, "zk_transpose_f16: leading dimension too small");
+  if ((cols + 63) / 64 > 0x7fffffff || (rows + 63) / 64 > 65535)
+    return fail(ZK_ERR_UNSUPPORTED, "zk_transpose_f16: matrix too large");
+  dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
+  transpose_f16_kernel<<<grid, 256, 0, as_stream(stream)>>>(
+      (const f16 *)src, (f16 *)dst, rows, cols, lds, ldd);
+  return check_launch("zk_transpose_f16");
+}

@@ -1,0 +1,233 @@
+"""BERT encoder on the zenith_amd kernels (fp16 and INT8-FFN variants).
+
+One post-LN layer is seven launches, in the reference encoder's order
+(benchmarks/bert_fp16_full.py:96-145, bert_hybrid.py:96-146) but fused:
+
+  1. QKV GEMM + bias            x[M,H] . Wqkv[3H,H]^T         -> qkv[M,3H]
+  2. flash attention            reads Q/K/V straight out of qkv by stride
+                                (no split/transpose kernels), writes ctx[M,H]
+  3. out-proj GEMM + bias       ctx . Wo^T                    -> t[M,H]
+  4. Add+LayerNorm              LN(t + x)                     -> h1[M,H]
+  5. FFN-up GEMM + bias + GELU  h1 . Wi^T                     -> u[M,4H]
+  6. FFN-down GEMM + bias       u . Wo2^T                     -> t[M,H]
+  7. Add+LayerNorm              LN(t + h1)                    -> out[M,H]
+
+The INT8-FFN variant replaces 5 and 6 by quantise -> int8 GEMM (dequant +
+bias + GELU epilogue) -> quantise -> int8 GEMM (dequant + bias epilogue).
+
+All activations live in buffers allocated once per (batch, seq); the whole
+forward can be captured into a HIP graph (torch.cuda.CUDAGraph) and replayed,
+which removes the ~84 host launches per forward from the critical path.
+Weights stay resident in HBM; 12 fp16 layers are ~170 MB.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import _lib as L
+
+F16 = torch.float16
+
+
+def _dev(a: np.ndarray, dtype, device) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device=device, dtype=dtype)
+
+
+def quantize_weight_per_channel(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Symmetric per-output-channel int8 weights: s[n] = max|W[n,:]| / 127,
+    q = clamp(round_half_even(W / s[n]), -128, 127) (host-side, once).
+    Reference rule: per-channel FakeQuantize (zenith/optimization/qat.py:
+    185-270) with the /127 scale of quantization.py:106."""
+    w = w.detach().to(torch.float32).cpu()
+    amax = w.abs().amax(dim=1)
+    s = torch.where(amax > 0, amax / 127.0, torch.ones_like(amax))
+    q = torch.clamp(torch.round(w / s[:, None]), -128, 127).to(torch.int8)
+    return q, s
+
+
+class BertEncoder:
+    """12-layer (by default) BERT encoder resident on one GPU.
+
+    layers: list of dicts of float32 numpy arrays with keys
+    Wq,bq,Wk,bk,Wv,bv,Wo,bo,ln1_g,ln1_b,Wi,bi,Wo2,bo2,ln2_g,ln2_b
+    (torch-Linear layout W[out, in]).
+    """
+
+    def __init__(self, layers: list[dict], heads: int = 12, eps: float = 1e-12,
+                 gelu: str = "erf", device: str | torch.device = "cuda"):
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise RuntimeError("BertEncoder runs on a GPU device")
+        L.load()  # fail loudly before any work if the kernels are missing
+        self.heads = heads
+        self.eps = float(eps)
+        self.gelu_epi = L.ZK_EPI_BIAS_GELU_ERF if gelu == "erf" else L.ZK_EPI_BIAS_GELU_TANH
+        self.hidden = layers[0]["Wq"].shape[1]
+        self.ffn = layers[0]["Wi"].shape[0]
+        if self.hidden % heads:
+            raise RuntimeError("hidden size must be a multiple of heads")
+        self.head_dim = self.hidden // heads
+        d = self.device
+        self.layers = []
+        for w in layers:
+            self.layers.append({
+                "Wqkv": _dev(np.concatenate([w["Wq"], w["Wk"], w["Wv"]], 0), F16, d),
+                "bqkv": _dev(np.concatenate([w["bq"], w["bk"], w["bv"]], 0), F16, d),
+                "Wo": _dev(w["Wo"], F16, d), "bo": _dev(w["bo"], F16, d),
+                "ln1_g": _dev(w["ln1_g"], F16, d), "ln1_b": _dev(w["ln1_b"], F16, d),
+                "Wi": _dev(w["Wi"], F16, d), "bi": _dev(w["bi"], F16, d),
+                "Wo2": _dev(w["Wo2"], F16, d), "bo2": _dev(w["bo2"], F16, d),
+                "ln2_g": _dev(w["ln2_g"], F16, d), "ln2_b": _dev(w["ln2_b"], F16, d),
+            })
+        self.int8 = None
+        self._bufs = None
+        self._graph = None
+
+    # ------------------------------------------------------------ INT8 FFN --
+    def enable_int8_ffn(self, s_x: list[float], s_h: list[float], layers_fp32: list[dict] | None = None):
+        """Switch the FFN to int8 with per-layer activation scales s_x (FFN-up
+        input) and s_h (GELU output); weights are quantised per output channel
+        from the fp32 masters if given, else from the resident fp16 weights."""
+        self.int8 = []
+        for i, lw in enumerate(self.layers):
+            if layers_fp32 is not None:
+                wi = torch.from_numpy(layers_fp32[i]["Wi"])
+                wo2 = torch.from_numpy(layers_fp32[i]["Wo2"])
+            else:
+                wi, wo2 = lw["Wi"], lw["Wo2"]
+            qi, si = quantize_weight_per_channel(wi)
+            qo, so = quantize_weight_per_channel(wo2)
+            self.int8.append({
+                "Wi_q": qi.to(self.device), "s_wi": si.to(self.device),
+                "Wo2_q": qo.to(self.device), "s_wo2": so.to(self.device),
+                "s_x": float(s_x[i]), "s_h": float(s_h[i]),
+            })
+        self._graph = None
+
+    def disable_int8_ffn(self):
+        self.int8 = None
+        self._graph = None
+
+    # ------------------------------------------------------------- buffers --
+    def _buffers(self, B: int, S: int):
+        key = (B, S)
+        if self._bufs is not None and self._bufs["key"] == key:
+            return self._bufs
+        M, H, I, d = B * S, self.hidden, self.ffn, self.device
+        self._bufs = {
+            "key": key,
+            "qkv": torch.empty((M, 3 * H), dtype=F16, device=d),
+            "ctx": torch.empty((M, H), dtype=F16, device=d),
+            "t": torch.empty((M, H), dtype=F16, device=d),
+            "h1": torch.empty((M, H), dtype=F16, device=d),
+            "u": torch.empty((M, I), dtype=F16, device=d),
+            "ping": torch.empty((M, H), dtype=F16, device=d),
+            "pong": torch.empty((M, H), dtype=F16, device=d),
+            "q_h": torch.empty((M, H), dtype=torch.int8, device=d),
+            "q_u": torch.empty((M, I), dtype=torch.int8, device=d),
+        }
+        self._graph = None
+        return self._bufs
+
+    # ------------------------------------------------------------- forward --
+    def _gemm(self, a, w, b, out, epi, residual=None, stream=None):
+        M, K = a.shape
+        N = w.shape[0]
+        L.call("zk_gemm_f16", a.data_ptr(), w.data_ptr(), out.data_ptr(), M, N, K,
+               a.stride(0), w.stride(0), out.stride(0), 1, L.ZK_F16, b.data_ptr(),
+               None if residual is None else residual.data_ptr(),
+               0 if residual is None else residual.stride(0), epi, stream)
+
+    def _layer(self, i: int, x: torch.Tensor, out: torch.Tensor, lens, B: int, S: int, stream):
+        w = self.layers[i]
+        bf = self._bufs
+        H, D, nh = self.hidden, self.head_dim, self.heads
+        M = B * S
+        qkv, ctx, t, h1, u = bf["qkv"], bf["ctx"], bf["t"], bf["h1"], bf["u"]
+        self._gemm(x, w["Wqkv"], w["bqkv"], qkv, L.ZK_EPI_BIAS, stream=stream)
+        base = qkv.data_ptr()
+        es = qkv.element_size()
+        ld = 3 * H
+        strides = L.strides_arg([S * ld, D, ld, S * ld, D, ld, S * ld, D, ld, S * H, D, H])
+        L.call("zk_flash_attn_fwd", base, base + H * es, base + 2 * H * es, ctx.data_ptr(),
+               B, nh, S, S, D, strides, None if lens is None else lens.data_ptr(),
+               float(1.0 / np.sqrt(D)), L.ZK_F16, stream)
+        self._gemm(ctx, w["Wo"], w["bo"], t, L.ZK_EPI_BIAS, stream=stream)
+        L.call("zk_layernorm", t.data_ptr(), x.data_ptr(), w["ln1_g"].data_ptr(),
+               w["ln1_b"].data_ptr(), h1.data_ptr(), M, H, self.eps, L.ZK_F16, stream)
+        if self.int8 is None:
+            self._gemm(h1, w["Wi"], w["bi"], u, self.gelu_epi, stream=stream)
+            self._gemm(u, w["Wo2"], w["bo2"], t, L.ZK_EPI_BIAS, stream=stream)
+        else:
+            q = self.int8[i]
+            qh, qu = bf["q_h"], bf["q_u"]
+            L.call("zk_quantize_i8", h1.data_ptr(), qh.data_ptr(), M * H, q["s_x"], L.ZK_F16, stream)
+            L.call("zk_gemm_i8", qh.data_ptr(), q["Wi_q"].data_ptr(), u.data_ptr(), M, self.ffn, H,
+                   H, H, self.ffn, q["s_x"], q["s_wi"].data_ptr(), w["bi"].data_ptr(), None, 0,
+                   self.gelu_epi, L.ZK_F16, stream)
+            L.call("zk_quantize_i8", u.data_ptr(), qu.data_ptr(), M * self.ffn, q["s_h"], L.ZK_F16, stream)
+            L.call("zk_gemm_i8", qu.data_ptr(), q["Wo2_q"].data_ptr(), t.data_ptr(), M, H, self.ffn,
+                   self.ffn, self.ffn, H, q["s_h"], q["s_wo2"].data_ptr(), w["bo2"].data_ptr(),
+                   None, 0, L.ZK_EPI_BIAS, L.ZK_F16, stream)
+        L.call("zk_layernorm", t.data_ptr(), h1.data_ptr(), w["ln2_g"].data_ptr(),
+               w["ln2_b"].data_ptr(), out.data_ptr(), M, H, self.eps, L.ZK_F16, stream)
+
+    def _run(self, x2: torch.Tensor, lens, B: int, S: int, out: torch.Tensor):
+        bf = self._bufs
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        cur = x2
+        n = len(self.layers)
+        for i in range(n):
+            dst = out if i == n - 1 else (bf["ping"] if i % 2 == 0 else bf["pong"])
+            self._layer(i, cur, dst, lens, B, S, stream)
+            cur = dst
+        return out
+
+    def _check(self, x: torch.Tensor, lens):
+        if x.dim() != 3 or x.shape[-1] != self.hidden:
+            raise RuntimeError(f"expected hidden states [batch, seq, {self.hidden}]")
+        if x.dtype != F16 or x.device != self.device:
+            raise RuntimeError("hidden states must be float16 on the encoder's device")
+        if lens is not None and (lens.dtype != torch.int32 or lens.numel() != x.shape[0]
+                                 or lens.device != self.device):
+            raise RuntimeError("lengths must be int32 [batch] on the encoder's device")
+
+    def forward(self, x: torch.Tensor, lengths: torch.Tensor | None = None) -> torch.Tensor:
+        """x [B, S, H] fp16 -> [B, S, H] fp16; lengths int32 [B] (key padding)."""
+        self._check(x, lengths)
+        B, S, H = x.shape
+        self._buffers(B, S)
+        x2 = x.contiguous().view(B * S, H)
+        out = torch.empty((B * S, H), dtype=F16, device=self.device)
+        self._run(x2, lengths, B, S, out)
+        return out.view(B, S, H)
+
+    __call__ = forward
+
+    # --------------------------------------------------------- HIP graph ----
+    def capture(self, B: int, S: int, with_lengths: bool = True):
+        """Capture one forward at (B, S) into a HIP graph with static input /
+        lengths / output tensors; returns (x_static, lens_static, out_static).
+        Fill x_static / lens_static, call replay(), read out_static."""
+        self._buffers(B, S)
+        self._gx = torch.zeros((B, S, self.hidden), dtype=F16, device=self.device)
+        self._gl = torch.full((B,), S, dtype=torch.int32, device=self.device) if with_lengths else None
+        self._go = torch.empty((B * S, self.hidden), dtype=F16, device=self.device)
+        x2 = self._gx.view(B * S, self.hidden)
+        # one eager pass so lazily-initialised state exists before capture
+        self._run(x2, self._gl, B, S, self._go)
+        torch.cuda.synchronize(self.device)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self._run(x2, self._gl, B, S, self._go)
+        torch.cuda.synchronize(self.device)
+        self._graph = g
+        return self._gx, self._gl, self._go.view(B, S, self.hidden)
+
+    def replay(self):
+        if self._graph is None:
+            raise RuntimeError("capture() first")
+        self._graph.replay()
+        return self._go.view(*self._gx.shape)
