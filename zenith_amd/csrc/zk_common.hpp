@@ -28,7 +28,7 @@ int fail(int code, const char *fmt, ...);
 // Check hipGetLastError() after a launch.
 int check_launch(const char *what);
 // 16-byte alignment of a device pointer.
-inline bool aligned16(const void *p) {
+__host__ __device__ inline bool aligned16(const void *p) {
   return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }

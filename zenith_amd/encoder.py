@@ -174,13 +174,14 @@ class BertEncoder:
         L.call("zk_layernorm", t.data_ptr(), h1.data_ptr(), w["ln2_g"].data_ptr(),
                w["ln2_b"].data_ptr(), out.data_ptr(), M, H, self.eps, L.ZK_F16, stream)
 
-    def _run(self, x2: torch.Tensor, lens, B: int, S: int, out: torch.Tensor):
+    def _run(self, x2: torch.Tensor, lens, B: int, S: int, out: torch.Tensor,
+             start: int = 0, stop: int | None = None):
         bf = self._bufs
         stream = torch.cuda.current_stream(self.device).cuda_stream
         cur = x2
-        n = len(self.layers)
-        for i in range(n):
-            dst = out if i == n - 1 else (bf["ping"] if i % 2 == 0 else bf["pong"])
+        stop = len(self.layers) if stop is None else stop
+        for i in range(start, stop):
+            dst = out if i == stop - 1 else (bf["ping"] if i % 2 == 0 else bf["pong"])
             self._layer(i, cur, dst, lens, B, S, stream)
             cur = dst
         return out
@@ -205,6 +206,18 @@ class BertEncoder:
         return out.view(B, S, H)
 
     __call__ = forward
+
+    def forward_layers(self, x: torch.Tensor, lengths: torch.Tensor | None,
+                       start: int, stop: int) -> torch.Tensor:
+        """Run layers [start, stop) only (same kernels as forward)."""
+        self._check(x, lengths)
+        if not 0 <= start < stop <= len(self.layers):
+            raise RuntimeError("bad layer range")
+        B, S, H = x.shape
+        self._buffers(B, S)
+        out = torch.empty((B * S, H), dtype=F16, device=self.device)
+        self._run(x.contiguous().view(B * S, H), lengths, B, S, out, start, stop)
+        return out.view(B, S, H)
 
     # --------------------------------------------------------- HIP graph ----
     def capture(self, B: int, S: int, with_lengths: bool = True):
