@@ -44,6 +44,31 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return 0.5f * x * (1.0f + tanhf(inner));
 }
 
+// Branch-free forms for GEMM epilogues (fp16 outputs).
+// erf by Abramowitz & Stegun 7.1.26: for z >= 0,
+//   erf(z) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-z^2),
+//   t = 1 / (1 + p z), |error| <= 1.5e-7.
+__device__ __forceinline__ float gelu_erf_fast(float x) {
+  const float z = fabsf(x) * 0.70710678118654752f;
+  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * z);
+  float q = 1.061405429f;
+  q = q * t - 1.453152027f;
+  q = q * t + 1.421413741f;
+  q = q * t - 0.284496736f;
+  q = q * t + 0.254829592f;
+  q *= t;
+  // 1 - erf(z), then GELU = 0.5 x (1 + sign(x) erf(|x| / sqrt 2))
+  const float tail = q * __builtin_amdgcn_exp2f(-z * z * 1.4426950408889634f);
+  return x >= 0.f ? x - 0.5f * x * tail : 0.5f * x * tail;
+}
+// tanh(y) = 1 - 2 / (1 + exp(2y)): exact identity, one exp and one reciprocal.
+__device__ __forceinline__ float gelu_tanh_fast(float x) {
+  const float y = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+  const float e = __builtin_amdgcn_exp2f(2.0f * 1.4426950408889634f * y);
+  const float th = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
+  return 0.5f * x * (1.0f + th);
+}
+
 // Butterfly sum / max across the 64 lanes of a wavefront.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -1,15 +1,33 @@
 // GEMMs for gfx950.
 //
-// zk_gemm_f16 / zk_gemm_i8: MFMA main loop shared by the fp16 and int8
-// paths. Both operands are K-major in memory (A[M,K], W[N,K]); each
-// workgroup owns a BM x BN output tile, 4 wavefronts in a 2 x 2 grid own
-// (BM/2) x (BN/2) sub-tiles built from 32x32 MFMA blocks. K is walked in
-// BKB-byte slices staged through two LDS buffers (one barrier per slice);
-// the next slice's 16-byte global loads are in flight while the current one
-// is multiplied. LDS rows are padded by 16 bytes so the row-strided 16-byte
-// fragment reads of a wavefront hit distinct banks. The epilogue (bias,
-// GELU, residual, int8 dequantisation) is applied to the accumulators before
-// the single store of C.
+// zk_gemm_f16 / zk_gemm_i8 share one MFMA kernel. Both operands are K-major
+// in memory (A[M,K], W[N,K]) and the kernel is byte-generic: an fp16 MFMA
+// step (32x32x16 or 16x16x32) and an int8 step (32x32x32 or 16x16x64) read
+// the same 16 bytes per lane and operand, so one LDS layout serves both.
+//
+// Workgroup: 4 wavefronts in a 2 x 2 grid, each owning a (BM/2) x (BN/2)
+// wave tile made of MS x MS MFMA blocks (MS = 32 or 16). The macro tile is
+// chosen per shape so that the BERT projections fill the 256 CUs in one
+// round (e.g. 256 x 192 tiles give exactly 256 tiles for M=4096, N=3072).
+//
+// K is walked in slices of BKB bytes per row. A slice of A and W goes from
+// global memory straight into LDS with buffer_load ... lds (16 bytes per
+// lane, 1 KB per wavefront instruction, no VGPR staging), into a ring of
+// ST stages; slices are issued ST-1 ahead, and each iteration has exactly
+// one barrier, preceded by an explicit vmcnt wait that leaves the younger
+// slices in flight. Rows are addressed through raw buffer descriptors that
+// end at the last valid row, so loads past M / N return zeros; chunks past
+// K are redirected out of range.
+//
+// LDS rows hold BKB bytes as 16-byte chunks; chunk c of row r sits at slot
+// c ^ f(r), with f spreading the 16 rows one fragment read touches over
+// 16 distinct 16-byte bank groups (a 256-byte bank period holds 2 rows of
+// 128 bytes or 4 rows of 64 bytes).
+//
+// Epilogue: each wavefront stages one MS-row stripe of its wave tile in
+// LDS as fp32 (after scale / bias / activation), then streams it out as
+// 8-column vectors, adding the residual on the way; no workgroup barrier is
+// needed between stripes.
 //
 // The B[K,N] (n-contiguous) layout of wmma_matmul is served by transposing B
 // once (zk_transpose_f16) into a caller-provided buffer; the Python layer
@@ -37,95 +55,185 @@ struct GemmParams {
   float s_x;
   const float *s_w;
   int tiles_n;
+  int tiles_m;
+  int group_m;
+};
+
+#define ZK_LDS(p) ((__attribute__((address_space(3))) void *)(p))
+
+// MFMA step on 16 bytes per lane and operand. MS = 32: lane l supplies row
+// l % 32, bytes [16 * (l / 32), +16) of the 32-byte k-step; the result
+// register r of lane l is D[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32].
+// MS = 16: lane l supplies row l % 16, bytes [16 * (l / 16), +16) of the
+// 64-byte k-step; register r is D[4 * (l / 16) + r][l % 16].
+template <int MS> struct F16Mma;
+template <> struct F16Mma<32> {
+  typedef f32x16 Acc;
+  static constexpr int R = 16;
+  static __device__ __forceinline__ Acc mma(f16x8 a, f16x8 b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct F16Mma<16> {
+  typedef f32x4 Acc;
+  static constexpr int R = 4;
+  static __device__ __forceinline__ Acc mma(f16x8 a, f16x8 b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <int MS> struct I8Mma;
+template <> struct I8Mma<32> {
+  typedef i32x16 Acc;
+  static constexpr int R = 16;
+  static __device__ __forceinline__ Acc mma(i32x4 a, i32x4 b, Acc c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct I8Mma<16> {
+  typedef i32x4 Acc;
+  static constexpr int R = 4;
+  static __device__ __forceinline__ Acc mma(i32x4 a, i32x4 b, Acc c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+  }
 };
 
 struct F16Op {
   typedef f16x8 Frag;
-  typedef f32x16 Acc;
+  template <int MS> using Mma = F16Mma<MS>;
   static constexpr int kElem = 2;
-  static __device__ __forceinline__ Acc mma(Frag a, Frag b, Acc c) {
-    return mfma32x32x16(a, b, c);
-  }
 };
 struct I8Op {
   typedef i32x4 Frag;
-  typedef i32x16 Acc;
+  template <int MS> using Mma = I8Mma<MS>;
   static constexpr int kElem = 1;
-  static __device__ __forceinline__ Acc mma(Frag a, Frag b, Acc c) {
-    return mfma32x32x32_i8(a, b, c);
-  }
 };
 
 template <typename T> __device__ __forceinline__ float to_f(T v) { return (float)v; }
 
 template <int EPI>
-__device__ __forceinline__ float epilogue(float v, float bias, float res) {
+__device__ __forceinline__ float epilogue(float v, float bias) {
   if (EPI == ZK_EPI_NONE) return v;
   v += bias;
-  if (EPI == ZK_EPI_BIAS_GELU_ERF) return gelu_erf(v);
-  if (EPI == ZK_EPI_BIAS_GELU_TANH) return gelu_tanh(v);
+  if (EPI == ZK_EPI_BIAS_GELU_ERF) return gelu_erf_fast(v);
+  if (EPI == ZK_EPI_BIAS_GELU_TANH) return gelu_tanh_fast(v);
   if (EPI == ZK_EPI_BIAS_RELU) return v > 0.f ? v : 0.f;
-  if (EPI == ZK_EPI_BIAS_RESIDUAL) return v + res;
-  return v;
+  return v;  // BIAS, BIAS_RESIDUAL (residual added at the store)
 }
 
-// Workgroup -> tile. The hardware deals workgroups round-robin over the 8
-// XCDs; renumbering so that each XCD receives a contiguous run of tiles
-// (same A rows, all N tiles) keeps that run's A and B slices in the XCD's
-// own L2.
-__device__ __forceinline__ int xcd_tile(int wg, int nwg) {
-  if ((nwg & 7) != 0) return wg;
-  return (wg & 7) * (nwg >> 3) + (wg >> 3);
+// Workgroup -> (tile_m, tile_n). The hardware deals workgroups round-robin
+// over the 8 XCDs; the index is first renumbered so that each XCD receives
+// a contiguous run, and the run is then laid out in groups of `group_m`
+// tile rows walked column by column, so one XCD's tiles form a compact
+// rectangle whose A rows and W rows stay in that XCD's L2.
+__device__ __forceinline__ void tile_of(int wg, int nwg, const GemmParams &p, int &tm, int &tn) {
+  int t = wg;
+  if ((nwg & 7) == 0) t = (wg & 7) * (nwg >> 3) + (wg >> 3);
+  const int per_group = p.group_m * p.tiles_n;
+  const int first_m = (t / per_group) * p.group_m;
+  const int gsz = min(p.tiles_m - first_m, p.group_m);
+  const int r = t % per_group;
+  tm = first_m + r % gsz;
+  tn = r / gsz;
 }
 
-// LDS tiles hold 128-byte K slices of BM (A) and BN (B) rows, unpadded; the
-// 16-byte chunk c of row r lives at chunk position c ^ (r & 7), so the 8 rows
-// a fragment read touches at one k fall on 8 different bank groups.
-__device__ __forceinline__ int swz(int row, int chunk) {
-  return row * 128 + ((chunk ^ (row & 7)) << 4);
+template <int BKB>
+__device__ __forceinline__ int lds_slot(int row, int c) {
+  return BKB == 128 ? (c ^ ((row >> 1) & 7)) : (c ^ ((row >> 2) & 3));
 }
 
-template <int BM, int BN>
-struct EpiTile {
-  static constexpr int ROWS = BM < 128 ? BM : 128;  // rows staged per pass
-  static constexpr int PITCH = BN + 8;                // fp32 words per LDS row
-  static constexpr int BYTES = ROWS * PITCH * 4;
-};
+constexpr int epi_pitch16(int w) {
+  int p = (w + 3) / 4 * 4;
+  while (p % 64 != 16 && p % 64 != 48) p += 4;
+  return p;
+}
 
-template <class OP, int BM, int BN, int WM, int WN>
+template <class OP, int BM, int BN, int MS, int BKB, int ST>
 struct GemmCfg {
-  static constexpr int NT = WM * WN * 64;
-  static constexpr int BKB = 128;  // bytes of K per stage
-  static constexpr int WTM = BM / WM, WTN = BN / WN;
-  static constexpr int TM = WTM / 32, TN = WTN / 32;
-  static constexpr int VA = BM * 8 / NT, VB = BN * 8 / NT;
+  static constexpr int NW = 4, NT = 256;
+  static constexpr int WTM = BM / 2, WTN = BN / 2;
+  static constexpr int TM = WTM / MS, TN = WTN / MS;
+  static constexpr int CH = BKB / 16;          // 16-byte chunks per LDS row
+  static constexpr int RPI = 1024 / BKB;       // rows per wavefront DMA instruction
+  static constexpr int IA = BM / RPI / NW;     // DMA instructions per wave per slice
+  static constexpr int IB = BN / RPI / NW;
   static constexpr int STAGE = (BM + BN) * BKB;
-  static constexpr int SMEM = (2 * STAGE > EpiTile<BM, BN>::BYTES) ? 2 * STAGE : EpiTile<BM, BN>::BYTES;
-  static_assert(BM * 8 % NT == 0 && BN * 8 % NT == 0, "tile/thread mismatch");
-  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be 32-aligned");
-  static_assert(EpiTile<BM, BN>::ROWS % WTM == 0 || WTM % EpiTile<BM, BN>::ROWS == 0, "epilogue pass");
+  static constexpr int KCH = MS == 32 ? 2 : 4;  // chunks per MFMA k-step
+  static constexpr int KS = CH / KCH;          // MFMA k-steps per slice
+  // fp32 words per epilogue LDS row, chosen so one register's worth of
+  // writes (32 columns x 2 rows 4 apart for MS = 32; 16 columns x 4
+  // consecutive rows for MS = 16) covers 64 distinct banks.
+  static constexpr int EPITCH = MS == 32 ? (WTN % 16 == 8 ? WTN : WTN + 8 - WTN % 16 + (WTN % 16 > 8 ? 16 : 0))
+                                         : epi_pitch16(WTN);
+  static constexpr int EPI_BYTES = NW * MS * EPITCH * 4;
+  static constexpr int SMEM = ST * STAGE > EPI_BYTES ? ST * STAGE : EPI_BYTES;
+  static_assert(BKB == 64 || BKB == 128, "slice width");
+  static_assert(WTM % MS == 0 && WTN % MS == 0, "wave tile must be a multiple of the MFMA block");
+  static_assert(BM % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "DMA split");
+  static_assert(KS >= 2 && KS % 2 == 0, "k-steps per slice must be even");
+  static_assert(ST >= 2 && (ST - 1) * (IA + IB) <= 63, "vmcnt range");
+  static_assert(SMEM <= 160 * 1024, "LDS budget");
+  static_assert(WTN % 8 == 0, "epilogue vectors");
 };
 
-// Two waves per SIMD: the register budget (256 per lane) holds the two
-// prefetch register sets, the fragments and the accumulators without spills.
-template <class OP, int BM, int BN, int WM, int WN, int EPI, typename OutT, bool DEQ>
-__global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void gemm_mfma_kernel(GemmParams p) {
-  typedef GemmCfg<OP, BM, BN, WM, WN> G;
-  constexpr int NT = G::NT, BKB = G::BKB, TM = G::TM, TN = G::TN;
-  constexpr int WTM = G::WTM, WTN = G::WTN, VA = G::VA, VB = G::VB;
-  __shared__ __attribute__((aligned(16))) char smem[G::SMEM];
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Wait until at most min(allowed, N) slices of PER instructions each are
+// still in flight (allowed is wave-uniform).
+template <int N, int PER>
+__device__ __forceinline__ void wait_slices(int allowed) {
+  if constexpr (N == 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (allowed >= N) wait_vmcnt<N * PER>();
+    else wait_slices<N - 1, PER>(allowed);
+  }
+}
+// Workgroup barrier without the fence __syncthreads() carries: the fence
+// would make the compiler wait for every outstanding LDS DMA, including the
+// slices deliberately left in flight. Completion of the slice about to be
+// read is established by the explicit vmcnt wait before it.
+// The wave's own outstanding LDS reads are completed first, so that a
+// stage every wave has issued its last reads of is safe to refill after it.
+// (The wait is the compiler-visible builtin, simm16 0xC07F = lgkmcnt(0)
+// with vmcnt and expcnt left open, so the compiler knows those fragment
+// registers are ready and adds no later wait on younger reads.)
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-  const int t = xcd_tile(blockIdx.x, gridDim.x);
-  const int tm = t / p.tiles_n, tn = t % p.tiles_n;
+// Scheduling hint for one k-step: NR LDS fragment reads spread evenly over
+// NM MFMAs (a read, then its share of MFMAs), so read latency hides under
+// matrix work instead of being waited for in front of it.
+template <int NR, int NM, int R = 0>
+__device__ __forceinline__ void interleave() {
+  if constexpr (R < NR) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    __builtin_amdgcn_sched_group_barrier(0x008, NM / NR + (R < NM % NR ? 1 : 0), 0);  // MFMA
+    interleave<NR, NM, R + 1>();
+  }
+}
+
+template <class OP, int BM, int BN, int MS, int BKB, int ST, int EPI, typename OutT, bool DEQ>
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
+  typedef GemmCfg<OP, BM, BN, MS, BKB, ST> G;
+  typedef typename OP::template Mma<MS> MM;
+  typedef typename OP::Frag Frag;
+  constexpr int TM = G::TM, TN = G::TN, IA = G::IA, IB = G::IB, CH = G::CH;
+  constexpr int WTM = G::WTM, WTN = G::WTN, KS = G::KS, KCH = G::KCH, R = MM::R;
+  __shared__ __attribute__((aligned(1024))) char smem[G::SMEM];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
+  const int wm = wave >> 1, wn = wave & 1;
+  int tm, tn;
+  tile_of(blockIdx.x, gridDim.x, p, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int64_t kbytes = (int64_t)p.K * OP::kElem;
-  // Raw buffer descriptors over this workgroup's A rows [m0, m0 + BM) and
-  // B rows [n0, n0 + BN): a load whose offset falls past the last valid row
-  // returns 0 in hardware, so edge tiles need no branches. K-tail chunks
-  // (k >= K inside a row) are redirected to an out-of-range offset.
+  const int kbytes = p.K * OP::kElem;
   const int64_t lda_b = p.lda * OP::kElem, ldb_b = p.ldb * OP::kElem;
   const int a_rows = min(BM, p.M - m0), b_rows = min(BN, p.N - n0);
   const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
@@ -134,193 +242,191 @@ void gemm_mfma_kernel(GemmParams p) {
   const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
       (void *)((const char *)p.B + (int64_t)n0 * ldb_b), (short)0,
       (int)((b_rows - 1) * ldb_b + kbytes), 0x00020000);
-  constexpr int OOB = 0x7ffffff0;
-  // thread -> (row = tid / 8 + v * NT / 8, 16-byte chunk = tid % 8): eight
-  // consecutive threads read one 128-byte row segment.
-  const int crow = tid >> 3, cchunk = (tid & 7) << 4;
-  const int a_off0 = (int)(crow * lda_b) + cchunk, a_step = (int)((NT / 8) * lda_b);
-  const int b_off0 = (int)(crow * ldb_b) + cchunk, b_step = (int)((NT / 8) * ldb_b);
 
-  const int kbytes32 = (int)kbytes;
-  auto load = [&](int kb, i32x4 (&ra)[VA], i32x4 (&rb)[VB]) {
-    const bool kin = kb + cchunk < kbytes32;
+  // DMA source offsets. Instruction g of this wave fills tile rows
+  // [(wave * I + g) * RPI, +RPI); lane l lands at LDS slot l % CH of row
+  // (l / CH) of that group and therefore fetches the logical chunk whose
+  // swizzled slot that is.
+  int offA[IA], chA[IA], offB[IB], chB[IB];
 #pragma unroll
-    for (int v = 0; v < VA; ++v)
-      ra[v] = __builtin_amdgcn_raw_buffer_load_b128(rA, kin ? a_off0 + v * a_step + kb : OOB, 0, 0);
+  for (int g = 0; g < IA; ++g) {
+    const int row = (wave * IA + g) * G::RPI + lane / CH;
+    const int c = lds_slot<BKB>(row, lane % CH);  // the swizzle is an involution
+    chA[g] = c * 16;
+    offA[g] = (int)(row * lda_b) + c * 16;
+  }
 #pragma unroll
-    for (int v = 0; v < VB; ++v)
-      rb[v] = __builtin_amdgcn_raw_buffer_load_b128(rB, kin ? b_off0 + v * b_step + kb : OOB, 0, 0);
-  };
-  auto stash = [&](int stage, const i32x4 (&ra)[VA], const i32x4 (&rb)[VB]) {
-    char *As = smem + stage * G::STAGE, *Bs = As + BM * BKB;
-#pragma unroll
-    for (int v = 0; v < VA; ++v) {
-      const int idx = tid + v * NT;
-      *(i32x4 *)(As + swz(idx >> 3, idx & 7)) = ra[v];
-    }
-#pragma unroll
-    for (int v = 0; v < VB; ++v) {
-      const int idx = tid + v * NT;
-      *(i32x4 *)(Bs + swz(idx >> 3, idx & 7)) = rb[v];
-    }
-  };
-
-  typename OP::Acc acc[TM][TN];
+  for (int g = 0; g < IB; ++g) {
+    const int row = (wave * IB + g) * G::RPI + lane / CH;
+    const int c = lds_slot<BKB>(row, lane % CH);
+    chB[g] = c * 16;
+    offB[g] = (int)(row * ldb_b) + c * 16;
+  }
+  typename MM::Acc acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+      for (int r = 0; r < R; ++r) acc[i][j][r] = 0;
 
-  // Fragments are double-buffered in registers: the reads for k-step ks+1
-  // are issued before the MFMAs of k-step ks.
-  constexpr int KS = BKB / 32;
-  auto compute = [&](int stage) {
-    const char *As = smem + stage * G::STAGE, *Bs = As + BM * BKB;
-    typename OP::Frag a[2][TM], b[2][TN];
-    auto rd = [&](int ks, typename OP::Frag (&fa)[TM], typename OP::Frag (&fb)[TN]) {
-      const int chunk = ks * 2 + (lane >> 5);
+  // Fragment row of this lane inside an MS-row block, and the chunk offset
+  // of its half / quarter of the k-step.
+  const int frow = lane % MS, fch = lane / MS;
+  // Fragments of two consecutive k-steps: k-step ks of every slice uses
+  // buffer ks & 1 (KS is even), so the first k-step of the next slice can
+  // be read while the last one of this slice is multiplied.
+  Frag fa[2][TM], fb[2][TN];
+  auto rd = [&](int stage, int ks, int buf) {
+    const char *As = smem + stage * G::STAGE;
+    const char *Bs = As + BM * BKB;
+    const int c = ks * KCH + fch;
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-        fa[i] = *(const typename OP::Frag *)(As + swz(wm * WTM + i * 32 + (lane & 31), chunk));
+    for (int i = 0; i < TM; ++i) {
+      const int row = wm * WTM + i * MS + frow;
+      fa[buf][i] = *(const Frag *)(As + row * BKB + lds_slot<BKB>(row, c) * 16);
+    }
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-        fb[j] = *(const typename OP::Frag *)(Bs + swz(wn * WTN + j * 32 + (lane & 31), chunk));
-    };
-    rd(0, a[0], b[0]);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      if (ks + 1 < KS) rd(ks + 1, a[(ks + 1) & 1], b[(ks + 1) & 1]);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = OP::mma(a[ks & 1][i], b[ks & 1][j], acc[i][j]);
+    for (int j = 0; j < TN; ++j) {
+      const int row = wn * WTN + j * MS + frow;
+      fb[buf][j] = *(const Frag *)(Bs + row * BKB + lds_slot<BKB>(row, c) * 16);
     }
   };
+  auto mma_step = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = MM::mma(fa[buf][i], fb[buf][j], acc[i][j]);
+  };
 
-  // Main loop: K slice kt is staged in LDS[kt % 2]; global loads run two
-  // slices ahead in one of two register sets. The steady-state loop is
-  // unrolled by two (statically named register sets) and contains no
-  // conditional load or stash, so every s_waitcnt in it waits only for the
-  // older register set; the last one to three slices are peeled.
-  const int nk = (int)((kbytes + BKB - 1) / BKB);
-  i32x4 ra0[VA], rb0[VB], ra1[VA], rb1[VB];
-  load(0, ra0, rb0);
-  if (nk > 1) load(BKB, ra1, rb1);
-  stash(0, ra0, rb0);
-  __syncthreads();
-  int kt = 0;
-  // sched_barrier(0) keeps the compiler from sinking the prefetch below the
-  // MFMAs (which would shorten the prefetch distance to one slice).
-  for (; kt + 3 < nk; kt += 2) {
-    load((kt + 2) * BKB, ra0, rb0);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(0);
-    __builtin_amdgcn_sched_barrier(0);
-    stash(1, ra1, rb1);
-    __syncthreads();
-    load((kt + 3) * BKB, ra1, rb1);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(1);
-    __builtin_amdgcn_sched_barrier(0);
-    stash(0, ra0, rb0);
-    __syncthreads();
+  const int nk = (kbytes + BKB - 1) / BKB;
+  // One K slice of A and W: IA + IB wavefront instructions, each moving
+  // 1 KB (64 lanes x 16 bytes) into consecutive LDS bytes. The host
+  // compilation pass sees an empty statement: its semantic check of this
+  // builtin with a run-time offset rejects the kernel, and clang would then
+  // silently omit the kernel's launch stub.
+#if defined(__HIP_DEVICE_COMPILE__)
+#define ZK_ISSUE(kt, stage)                                                                   \
+  do {                                                                                        \
+    const int kb_ = (kt) * BKB;                                                               \
+    char *as_ = smem + (stage) * G::STAGE, *bs_ = as_ + BM * BKB;                             \
+    _Pragma("unroll") for (int g = 0; g < IA; ++g)                                            \
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(                                             \
+            rA, ZK_LDS(as_ + (wave * IA + g) * 1024), 16,                                     \
+            kb_ + chA[g] < kbytes ? offA[g] + kb_ : 0x7ffffff0, 0, 0, 0);                     \
+    _Pragma("unroll") for (int g = 0; g < IB; ++g)                                            \
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(                                             \
+            rB, ZK_LDS(bs_ + (wave * IB + g) * 1024), 16,                                     \
+            kb_ + chB[g] < kbytes ? offB[g] + kb_ : 0x7ffffff0, 0, 0, 0);                     \
+  } while (0)
+#else
+#define ZK_ISSUE(kt, stage) ((void)(kt), (void)(stage))
+#endif
+  // Prologue: one slice per stage.
+#pragma unroll
+  for (int s = 0; s < ST; ++s)
+    if (s < nk) ZK_ISSUE(s, s);
+  wait_slices<ST - 1, IA + IB>(nk - 1);
+  lds_barrier();
+  rd(0, 0, 0);
+  // Main loop over slices. Before the last k-step of slice kt every wave
+  // waits for slice kt + 1 and meets at the barrier; by then the ring stage
+  // of slice kt has been read completely (its last fragments are in
+  // registers), so slice kt + ST is issued into it, and the first
+  // fragments of slice kt + 1 are read under the last MFMAs of slice kt.
+  auto steps_but_last = [&](int stage) {
+#pragma unroll
+    for (int ks = 0; ks + 1 < KS; ++ks) {
+      rd(stage, ks + 1, (ks + 1) & 1);
+      mma_step(ks & 1);
+      interleave<TM + TN, TM * TN>();
+    }
+  };
+  int stage = 0;
+  for (int kt = 0; kt + 1 < nk; ++kt) {
+    steps_but_last(stage);
+    const int next = stage + 1 == ST ? 0 : stage + 1;
+    wait_slices<ST - 2, IA + IB>(nk - 2 - kt);
+    lds_barrier();
+    if (kt + ST < nk) ZK_ISSUE(kt + ST, stage);
+    rd(next, 0, 0);
+    mma_step(1);
+    interleave<TM + TN, TM * TN>();
+    stage = next;
   }
-  const int rem = nk - kt;  // 1, 2 or 3 slices left; slice kt is in LDS[0]
-  if (rem == 3) {
-    load((kt + 2) * BKB, ra0, rb0);
-    compute(0);
-    stash(1, ra1, rb1);
-    __syncthreads();
-    compute(1);
-    stash(0, ra0, rb0);
-    __syncthreads();
-    compute(0);
-  } else if (rem == 2) {
-    compute(0);
-    stash(1, ra1, rb1);
-    __syncthreads();
-    compute(1);
-  } else {
-    compute(0);
-  }
-  __syncthreads();
+  steps_but_last(stage);  // last slice: nothing left to prefetch
+  mma_step(1);
+#undef ZK_ISSUE
+  __syncthreads();  // every wave is done reading the ring; it becomes epilogue space
 
-  // Epilogue, in passes of EpiTile::ROWS rows: waves write their scaled /
-  // biased / activated accumulators into an fp32 LDS tile (lane: column
-  // lane % 32, rows 8*(r/4) + 4*(lane/32) + r%4 of each 32x32 block), then
-  // all threads stream the tile out as 8-column vectors, adding the residual
-  // on the way.
-  typedef EpiTile<BM, BN> E;
-  float *Cs = (float *)smem;
+  // Epilogue: per wave, one MS-row stripe at a time.
+  float *ws = (float *)smem + wave * MS * G::EPITCH;
   OutT *C = (OutT *)p.C;
   const OutT *bias = (const OutT *)p.bias;
   const OutT *res = (const OutT *)p.res;
   const bool vec_ok = (p.ldc % 8 == 0) && aligned16(p.C) &&
                       (EPI != ZK_EPI_BIAS_RESIDUAL || ((p.ldr % 8 == 0) && aligned16(p.res)));
+  float bj[TN], sj[TN];
 #pragma unroll
-  for (int pass = 0; pass < BM / E::ROWS; ++pass) {
-    const int prow0 = pass * E::ROWS;
+  for (int j = 0; j < TN; ++j) {
+    const int col = n0 + wn * WTN + j * MS + frow;
+    bj[j] = 0.f;
+    sj[j] = 1.f;
+    if (col < p.N) {
+      if (EPI != ZK_EPI_NONE) bj[j] = to_f(bias[col]);
+      if (DEQ) sj[j] = p.s_x * p.s_w[col];
+    }
+  }
+  constexpr int VPR = WTN / 8;  // 8-column vectors per stripe row
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int ncol = wn * WTN + j * 32 + (lane & 31);
-      const int col = n0 + ncol;
-      float b = 0.f, sc = 1.f;
-      if (col < p.N) {
-        if (EPI != ZK_EPI_NONE) b = to_f(bias[col]);
-        if (DEQ) sc = p.s_x * p.s_w[col];
-      }
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int mbase = wm * WTM + i * 32;
-        if (mbase < prow0 || mbase >= prow0 + E::ROWS) continue;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int mloc = mbase - prow0 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-          if constexpr (std::is_same<OutT, int32_t>::value) {
-            ((int *)Cs)[mloc * E::PITCH + ncol] = acc[i][j][r];
-          } else {
-            const float v = DEQ ? (float)acc[i][j][r] * sc : (float)acc[i][j][r];
-            Cs[mloc * E::PITCH + ncol] = epilogue<EPI == ZK_EPI_BIAS_RESIDUAL ? ZK_EPI_BIAS : EPI>(v, b, 0.f);
-          }
+      for (int r = 0; r < R; ++r) {
+        const int rl = MS == 32 ? 8 * (r >> 2) + 4 * fch + (r & 3) : 4 * fch + r;
+        float *dst = ws + rl * G::EPITCH + j * MS + frow;
+        if constexpr (std::is_same<OutT, int32_t>::value) {
+          *(int *)dst = acc[i][j][r];
+        } else {
+          const float v = DEQ ? (float)acc[i][j][r] * sj[j] : (float)acc[i][j][r];
+          *dst = epilogue<EPI>(v, bj[j]);
         }
       }
     }
-    __syncthreads();
-    constexpr int GPR = BN / 8;  // 8-column groups per row
-    for (int g = tid; g < E::ROWS * GPR; g += NT) {
-      const int rl = g / GPR, cl = (g % GPR) * 8;
-      const int row = m0 + prow0 + rl, col = n0 + cl;
+    const int row0 = m0 + wm * WTM + i * MS, col0 = n0 + wn * WTN;
+    for (int v = lane; v < MS * VPR; v += 64) {
+      const int rl = v / VPR, cl = (v % VPR) * 8;
+      const int row = row0 + rl, col = col0 + cl;
       if (row >= p.M || col >= p.N) continue;
-      const float *src = Cs + rl * E::PITCH + cl;
+      const float *src = ws + rl * G::EPITCH + cl;
       OutT *dst = C + (int64_t)row * p.ldc + col;
       if (vec_ok && col + 8 <= p.N) {
-        f32x4 lo = *(const f32x4 *)src, hi = *(const f32x4 *)(src + 4);
+        const f32x4 lo = *(const f32x4 *)src, hi = *(const f32x4 *)(src + 4);
         if constexpr (std::is_same<OutT, int32_t>::value) {
           *(f32x4 *)dst = lo;  // raw bits of the int32 accumulators
           *(f32x4 *)(dst + 4) = hi;
         } else {
-          float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          float o[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
           if constexpr (EPI == ZK_EPI_BIAS_RESIDUAL) {
             const OutT *rp = res + (int64_t)row * p.ldr + col;
             if constexpr (std::is_same<OutT, f16>::value) {
               const f16x8 rv = *(const f16x8 *)rp;
 #pragma unroll
-              for (int e = 0; e < 8; ++e) v[e] += (float)rv[e];
+              for (int e = 0; e < 8; ++e) o[e] += (float)rv[e];
             } else {
 #pragma unroll
-              for (int e = 0; e < 8; ++e) v[e] += to_f(rp[e]);
+              for (int e = 0; e < 8; ++e) o[e] += to_f(rp[e]);
             }
           }
           if constexpr (std::is_same<OutT, f16>::value) {
-            f16x8 o;
+            f16x8 h;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] = (f16)v[e];
-            *(f16x8 *)dst = o;
+            for (int e = 0; e < 8; ++e) h[e] = (f16)o[e];
+            *(f16x8 *)dst = h;
           } else {
-            *(f32x4 *)dst = f32x4{v[0], v[1], v[2], v[3]};
-            *(f32x4 *)(dst + 4) = f32x4{v[4], v[5], v[6], v[7]};
+            *(f32x4 *)dst = f32x4{o[0], o[1], o[2], o[3]};
+            *(f32x4 *)(dst + 4) = f32x4{o[4], o[5], o[6], o[7]};
           }
         }
       } else {
@@ -328,24 +434,38 @@ void gemm_mfma_kernel(GemmParams p) {
           if constexpr (std::is_same<OutT, int32_t>::value) {
             dst[e] = ((const int *)src)[e];
           } else {
-            float v = src[e];
-            if (EPI == ZK_EPI_BIAS_RESIDUAL) v += to_f(res[(int64_t)row * p.ldr + col + e]);
-            dst[e] = (OutT)v;
+            float o = src[e];
+            if (EPI == ZK_EPI_BIAS_RESIDUAL) o += to_f(res[(int64_t)row * p.ldr + col + e]);
+            dst[e] = (OutT)o;
           }
         }
       }
     }
-    __syncthreads();
   }
 }
 
 // ------------------------------------------------------------ dispatch ----
-template <class OP, int BM, int BN, int WM, int WN, typename OutT, bool DEQ>
+// Tile configurations (BM, BN, MS, BKB, ST); measured on MI355X at the BERT
+// projection shapes and at squares (the choice rule is in pick_cfg).
+//   0: 256x256, 32x32 MFMA, 64-byte slices, 4 stages (128 KB ring, 1 WG/CU)
+//   1: 128x128, 32x32, 128-byte slices, 2 stages (64 KB)
+//   2: 128x96,  16x16, 128-byte slices, 2 stages (56 KB)
+//   3: 64x64,   16x16, 128-byte slices, 2 stages (32 KB, up to 5 WG/CU)
+//   4: 128x96,  16x16, 128-byte slices, 4 stages (112 KB)
+constexpr int kNumCfgs = 5;
+
+template <class OP, int BM, int BN, int MS, int BKB, int ST, typename OutT, bool DEQ>
 static void launch_epi(GemmParams p, int epi, hipStream_t s) {
   p.tiles_n = (p.N + BN - 1) / BN;
-  const int grid = ((p.M + BM - 1) / BM) * p.tiles_n;
-  constexpr int NT = WM * WN * 64;
-#define ZK_L(E) gemm_mfma_kernel<OP, BM, BN, WM, WN, E, OutT, DEQ><<<grid, NT, 0, s>>>(p)
+  p.tiles_m = (p.M + BM - 1) / BM;
+  const int grid = p.tiles_m * p.tiles_n;
+  // tile rows per group: enough that one XCD's share of the grid is a
+  // rectangle about as tall as it is wide
+  int gm = 1;
+  const int per_xcd = (grid + 7) / 8;
+  while (gm * 2 <= p.tiles_m && gm * gm * 4 <= per_xcd) gm *= 2;
+  p.group_m = gm;
+#define ZK_L(E) gemm_mfma_kernel<OP, BM, BN, MS, BKB, ST, E, OutT, DEQ><<<grid, 256, 0, s>>>(p)
   switch (epi) {
     case ZK_EPI_NONE: ZK_L(ZK_EPI_NONE); break;
     case ZK_EPI_BIAS: ZK_L(ZK_EPI_BIAS); break;
@@ -357,30 +477,34 @@ static void launch_epi(GemmParams p, int epi, hipStream_t s) {
 #undef ZK_L
 }
 
-// Tile configurations (BM x BN, waves WM x WN; every wave owns 64x64 except
-// cfg 3, whose waves own 32x64):
-//   0: 128x128, 2x2 (256 threads)    1: 256x128, 4x2 (512 threads)
-//   2: 128x256, 2x4 (512 threads)    3:  64x128, 2x2 (256 threads)
-static int pick_cfg(int M, int N) {
+// Shape -> configuration, from measurements at M = 4096:
+//   N <= 1024 (out-projection, FFN-down): many small tiles keep every CU
+//     busy; 64x64 for short K, the deep-ring 128x96 for K >= 2048;
+//   N >= 2048: 128x128 once that gives >= 640 tiles (FFN-up), else 128x96
+//     (QKV); very large problems take 256x256.
+// ZK_GEMM_CFG=<id> forces a configuration (tuning runs).
+static int pick_cfg(int M, int N, int K) {
   static int forced = -2;
   if (forced == -2) {
     const char *e = getenv("ZK_GEMM_CFG");
     forced = e ? atoi(e) : -1;
   }
-  if (forced >= 0 && forced <= 3) return forced;
-  auto tiles = [&](int bm, int bn) { return (int64_t)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-  if (tiles(256, 128) >= 256) return 1;
-  if (tiles(128, 128) >= 192) return 0;
-  return 3;
+  if (forced >= 0 && forced < kNumCfgs) return forced;
+  const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+  if (t128 >= 2048) return 0;
+  if (N <= 1024) return K >= 2048 ? 4 : 3;
+  if (t128 >= 640) return 1;
+  return 2;
 }
 
 template <class OP, typename OutT, bool DEQ>
 static void launch_mfma(GemmParams p, int epi, hipStream_t s) {
-  switch (pick_cfg(p.M, p.N)) {
-    case 0: launch_epi<OP, 128, 128, 2, 2, OutT, DEQ>(p, epi, s); break;
-    case 1: launch_epi<OP, 256, 128, 4, 2, OutT, DEQ>(p, epi, s); break;
-    case 2: launch_epi<OP, 128, 256, 2, 4, OutT, DEQ>(p, epi, s); break;
-    default: launch_epi<OP, 64, 128, 2, 2, OutT, DEQ>(p, epi, s); break;
+  switch (pick_cfg(p.M, p.N, p.K)) {
+    case 0: launch_epi<OP, 256, 256, 32, 64, 4, OutT, DEQ>(p, epi, s); break;
+    case 1: launch_epi<OP, 128, 128, 32, 128, 2, OutT, DEQ>(p, epi, s); break;
+    case 2: launch_epi<OP, 128, 96, 16, 128, 2, OutT, DEQ>(p, epi, s); break;
+    case 4: launch_epi<OP, 128, 96, 16, 128, 4, OutT, DEQ>(p, epi, s); break;
+    default: launch_epi<OP, 64, 64, 16, 128, 2, OutT, DEQ>(p, epi, s); break;
   }
 }
 
