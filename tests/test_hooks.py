@@ -1,0 +1,245 @@
+"""Graph hooks on the CPU: FX pattern rewrites (which nodes become HIP
+calls), registry selection rules, dispatcher argument marshalling and the
+compile-backend gating. No kernel runs here; the GPU side of the same hooks
+is tests/test_gpu_hooks.py.
+
+Reference behaviour mirrored: pattern registry and FXOptimizer surface
+(tests/python/test_fx_patterns.py:13-203), registry priority / precision
+fallback (zenith/runtime/kernel_registry.py:118-153, tested in
+tests/test_numerical_accuracy.py:86-117), dispatcher marshalling
+(zenith/runtime/dispatcher.py:235-315)."""
+
+import torch
+import torch.fx
+import torch.nn.functional as F
+import pytest
+
+from zenith_amd.hooks import backend, fx_optimizer as O, fx_patterns as P
+from zenith_amd.hooks.dispatcher import (ExecutionContext, KernelDispatcher, Node,
+                                         UnsupportedOperationError)
+from zenith_amd.hooks.kernel_registry import KernelRegistry, KernelSpec, Precision
+
+
+# ------------------------------------------------------------ patterns ----
+def test_pattern_registry_surface():
+    names = [p.name for p in P.get_all_patterns()]
+    for n in ("sdpa_to_flash", "gelu_tanh_to_native", "manual_layernorm_to_native"):
+        assert n in names
+    for p in P.get_all_patterns():
+        assert isinstance(p, P.FXPattern) and callable(p.pattern_fn) and callable(p.replacement_fn)
+    assert isinstance(P.is_zenith_cuda_available(), bool)
+
+
+def test_pattern_functions_compute_their_op():
+    """The pattern bodies are the ops they claim (the reference's own
+    pattern tests, test_fx_patterns.py:151-203)."""
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(2, 3, 8, 16, generator=g) for _ in range(3))
+    torch.testing.assert_close(P.sdpa_pattern(q, k, v), F.scaled_dot_product_attention(q, k, v),
+                               rtol=1e-5, atol=1e-6)
+    x = torch.randn(4, 64, generator=g)
+    torch.testing.assert_close(P.gelu_tanh_pattern(x), F.gelu(x, approximate="tanh"),
+                               rtol=1e-5, atol=1e-6)
+    w, b = torch.randn(64, generator=g), torch.randn(64, generator=g)
+    torch.testing.assert_close(P.layernorm_pattern(x, w, b), F.layer_norm(x, (64,), w, b),
+                               rtol=1e-5, atol=1e-5)
+
+
+class _Manual(torch.nn.Module):
+    """Reference-style written-out attention / GELU / LayerNorm."""
+
+    def __init__(self):
+        super().__init__()
+        self.w = torch.nn.Parameter(torch.randn(64, 32))
+        self.b = torch.nn.Parameter(torch.randn(64))
+        self.g = torch.nn.Parameter(torch.ones(32))
+        self.be = torch.nn.Parameter(torch.zeros(32))
+
+    def forward(self, q, k, v, x, r):
+        scale = q.shape[-1] ** -0.5
+        a = F.softmax(torch.matmul(q, k.transpose(-2, -1)) * scale, dim=-1)
+        o = torch.matmul(a, v)
+        h = F.gelu(F.linear(x, self.w, self.b))
+        t = 0.5 * x * (1.0 + torch.tanh(0.7978845608028654 * (x + 0.044715 * torch.pow(x, 3))))
+        mean = t.mean(dim=-1, keepdim=True)
+        var = t.var(dim=-1, keepdim=True, unbiased=False)
+        ln = (t - mean) / torch.sqrt(var + 1e-5) * self.g + self.be
+        return o, h, ln
+
+
+class _Modules(torch.nn.Module):
+    """Module / functional forms (what real encoders and dynamo graphs hold)."""
+
+    def __init__(self):
+        super().__init__()
+        self.up = torch.nn.Linear(32, 64)
+        self.act = torch.nn.GELU()
+        self.ln = torch.nn.LayerNorm(64, eps=1e-12)
+        self.proj = torch.nn.Linear(64, 64)
+        self.ln2 = torch.nn.LayerNorm(64)
+
+    def forward(self, x, r, q, k, v):
+        a = F.scaled_dot_product_attention(q, k, v)
+        h = self.ln(self.act(self.up(x)) + r)
+        m = F.scaled_dot_product_attention(q, k, v, attn_mask=torch.ones(8, 8, dtype=torch.bool))
+        return a, self.ln2(self.proj(h)), F.gelu(h, approximate="tanh"), m
+
+
+def _opt(mod, **kw):
+    gm = torch.fx.symbolic_trace(mod)
+    opt = O.FXOptimizer(require_gpu_inputs=False, strict=True, **kw)
+    return opt.optimize(gm), opt.get_stats()
+
+
+def test_reference_patterns_rewrite_to_hip_calls():
+    gm, st = _opt(_Manual())
+    assert sorted(O.replaced_targets(gm)) == sorted(
+        ["hip_flash_attention", "hip_linear_gelu", "hip_gelu_tanh", "hip_layernorm"])
+    assert st.patterns_failed == 0
+    # nothing of the written-out forms is left
+    left = {n.target for n in gm.graph.nodes if n.op == "call_function"}
+    assert F.softmax not in left and torch.tanh not in left and torch.sqrt not in left
+
+
+def test_structural_rewrites_modules_and_functionals():
+    gm, st = _opt(_Modules())
+    t = O.replaced_targets(gm)
+    assert t.count("hip_linear_gelu") == 1          # up + GELU fused
+    assert t.count("hip_add_layernorm_eps") == 1    # residual + LN fused
+    assert t.count("hip_linear") == 1 and t.count("hip_layernorm") == 1
+    assert t.count("hip_gelu_tanh") == 1
+    assert t.count("hip_flash_attention") == 1      # masked SDPA left as is
+    assert any(n.target is F.scaled_dot_product_attention for n in gm.graph.nodes)
+    # eps of the module is carried over
+    ln = [n for n in gm.graph.nodes if getattr(n.target, "__name__", "") == "hip_add_layernorm_eps"][0]
+    assert ln.args[-1] == 1e-12
+
+
+def test_group_switches_and_cpu_inputs_skip():
+    gm, st = _opt(_Modules(), enable_attention=False, enable_activation=False,
+                  enable_normalization=False, enable_linear=False)
+    assert O.replaced_targets(gm) == []
+    gm = torch.fx.symbolic_trace(_Modules())
+    opt = O.FXOptimizer()
+    opt.optimize(gm, [torch.zeros(2, 32)])
+    assert opt.get_stats().skipped_reason and O.replaced_targets(gm) == []
+
+
+def test_rewritten_graph_refuses_cpu_tensors():
+    """The HIP leaves never fall back to torch: CPU tensors raise."""
+    gm, _ = _opt(_Modules())
+    args = (torch.randn(4, 32), torch.randn(4, 64), *(torch.randn(1, 2, 8, 64) for _ in range(3)))
+    with pytest.raises(RuntimeError):
+        gm(*args)
+
+
+def test_backend_gating():
+    b = backend.create_compile_backend(opt_level=1)
+    gm = torch.fx.symbolic_trace(_Modules())
+    assert b(gm, []) == gm.forward
+    b2 = backend.create_compile_backend()  # default level 2 rewrites
+    gm2 = torch.fx.symbolic_trace(_Modules())
+    fwd = b2(gm2, [])
+    assert fwd.__self__ is gm2 and len(O.replaced_targets(gm2)) >= 5
+
+
+# ------------------------------------------------------------ registry ----
+def _spec(name, ops, prec, prio, fn=None, **kw):
+    return KernelSpec(name=name, op_types=ops, precision=prec, kernel_fn=fn or (lambda *a: name),
+                      priority=prio, **kw)
+
+
+def test_registry_priority_and_precision_fallback():
+    reg = KernelRegistry()
+    reg.register(_spec("low", ["Linear"], Precision.FP32, 1))
+    reg.register(_spec("high", ["Linear"], Precision.FP32, 25))
+    reg.register(_spec("mid16", ["Linear"], Precision.FP16, 10))
+    assert reg.get_kernel("Linear", Precision.FP32).name == "high"
+    assert reg.get_kernel("Linear", Precision.FP16).name == "mid16"
+    assert reg.get_kernel("Linear", Precision.BF16).name == "high"  # falls back to FP32
+    assert reg.get_kernel("Conv", Precision.FP32) is None
+    assert reg.is_supported("Linear", Precision.FP16) and not reg.is_supported("Linear", Precision.INT8)
+    assert reg.get_kernel("Linear", Precision.FP32).function is reg.get_kernel("Linear", Precision.FP32).kernel_fn
+
+
+def test_registry_constraints():
+    reg = KernelRegistry()
+    reg.register(_spec("small", ["Attention"], Precision.FP16, 30, input_constraints={"max_seq_len": 128}))
+    reg.register(_spec("any", ["Attention"], Precision.FP16, 5))
+    assert reg.get_kernel("Attention", Precision.FP16, [(2, 128, 64)]).name == "small"
+    assert reg.get_kernel("Attention", Precision.FP16, [(2, 512, 64)]).name == "any"
+
+
+def test_hip_registry_needs_the_library(tmp_path, monkeypatch):
+    """initialize() registers only HIP kernels; every fused op type the graph
+    passes emit has one."""
+    reg = KernelRegistry()
+    reg.initialize()
+    for op in ("Linear", "Gemm", "MatMul", "LayerNorm", "FusedAddLayerNorm", "AddLayerNorm",
+               "FusedBiasGeLU", "LinearGelu", "QKVProjection", "FlashAttention", "Attention",
+               "FusedAttentionEpilogue", "FusedFFN", "Gelu", "Relu"):
+        k = reg.get_kernel(op, Precision.FP16)
+        assert k is not None and k.priority == 25 and k.name.startswith("hip_"), op
+    assert reg.get_kernel("Linear", Precision.INT8).name.startswith("hip_qlinear")
+
+
+# ---------------------------------------------------------- dispatcher ----
+class _Rec:
+    def __init__(self):
+        self.calls = []
+
+    def __call__(self, name):
+        def fn(*args, **kw):
+            self.calls.append((name, args, kw))
+            return name
+        return fn
+
+
+def _disp(rec, prec=Precision.FP32):
+    reg = KernelRegistry()
+    for op in ("Linear", "MatMul", "LayerNorm", "FusedAddLayerNorm", "GELU", "FusedBiasGeLU",
+               "Attention", "FlashAttention", "QKVProjection", "FusedFFN", "LinearGelu"):
+        reg.register(_spec(op, [op], prec, 25, fn=rec(op)))
+    return KernelDispatcher(registry=reg, precision=prec)
+
+
+def test_dispatcher_linear_layouts():
+    rec = _Rec()
+    d = _disp(rec)
+    x, W, B, b = torch.zeros(2, 3), torch.zeros(4, 3), torch.zeros(3, 4), torch.zeros(4)
+    ctx = ExecutionContext({"x": x, "y": torch.zeros(3, 5)})
+    d.dispatch(Node("Linear", ["x"], ["o1"]), ctx, {"weight": W, "bias": b})
+    d.dispatch(Node("Gemm", ["x"], ["o2"], {"transB": 1}), ctx, {"B": W, "C": b})
+    d.dispatch(Node("Gemm", ["x"], ["o3"]), ctx, {"B": B, "C": b})
+    d.dispatch(Node("MatMul", ["x"], ["o4"]), ctx, {"B": B})
+    d.dispatch(Node("MatMul", ["x", "y"], ["o5"]), ctx)
+    shapes = [(c[0], tuple(c[1][1].shape)) for c in rec.calls]
+    # every weighted form reaches the kernel as W[N, K]; two activations stay A . B
+    assert shapes == [("Linear", (4, 3)), ("Linear", (4, 3)), ("Linear", (4, 3)),
+                      ("Linear", (4, 3)), ("MatMul", (3, 5))]
+    assert ctx.get_tensor("o1") == "Linear" and d.get_dispatch_stats()["total_dispatches"] == 5
+
+
+def test_dispatcher_fused_ops_and_eps():
+    rec = _Rec()
+    d = _disp(rec, Precision.FP16)
+    t = torch.zeros(2, 4)
+    ctx = ExecutionContext({"a": t, "r": t, "q": t, "k": t, "v": t, "lens": torch.zeros(2)})
+    d.dispatch(Node("LayerNormalization", ["a"], ["o"], {"epsilon": 1e-12}), ctx,
+               {"gamma": t[0], "beta": t[0]})
+    d.dispatch(Node("AddLayerNorm", ["a", "r"], ["o"]), ctx, {"gamma": t[0], "beta": t[0]})
+    d.dispatch(Node("Gelu", ["a"], ["o"], {"approximate": "none"}), ctx)
+    d.dispatch(Node("FlashAttention", ["q", "k", "v", "lens"], ["o"], {"scale": 0.125}), ctx)
+    d.dispatch(Node("QKVProjection", ["a"], ["q2", "k2", "v2"]), ctx,
+               {"Wq": t, "bq": t[0], "Wk": t, "bk": t[0], "Wv": t, "bv": t[0]})
+    names = [c[0] for c in rec.calls]
+    assert names == ["LayerNorm", "FusedAddLayerNorm", "GELU", "FlashAttention", "QKVProjection"]
+    assert rec.calls[0][1][3] == 1e-12 and rec.calls[1][1][4] == 1e-5
+    assert rec.calls[2][1][1] == "none"
+    assert rec.calls[3][2] == {"key_padding_lengths": ctx.get_tensor("lens"), "scale": 0.125}
+
+
+def test_dispatcher_unsupported():
+    d = _disp(_Rec())
+    with pytest.raises(UnsupportedOperationError):
+        d.dispatch(Node("Conv", ["a"], ["o"]), ExecutionContext({"a": torch.zeros(1)}))

@@ -13,17 +13,26 @@ Differences:
   - a graph whose example inputs are not CUDA tensors is left untouched
     (the replacements are HIP kernels); `stats.skipped_reason` says why;
   - a failure inside the rewriter is counted and re-raised when
-    `strict=True` instead of being swallowed.
+    `strict=True` instead of being swallowed;
+  - plain Linear layers (`enable_linear`, default on) go to the HIP GEMM;
+  - after the subgraph patterns, a structural pass rewrites the forms real
+    models and torch.compile graphs contain, which the literal patterns
+    cannot match: nn.Linear / nn.LayerNorm / nn.GELU modules, F.layer_norm
+    with a constant normalized shape, F.scaled_dot_product_attention
+    without mask or dropout. Where the graph carries shape metadata, an
+    attention whose head_dim the kernel does not support is left alone.
 """
 
 from __future__ import annotations
 
 import logging
+import operator
 from dataclasses import dataclass, field
 from typing import Any, Optional
 
 import torch
 import torch.fx
+import torch.nn.functional as F
 from torch.fx import subgraph_rewriter
 
 from . import fx_patterns as P
@@ -52,13 +61,15 @@ def _on_gpu(example_inputs) -> bool:
 class FXOptimizer:
     def __init__(self, enable_attention: bool = True, enable_activation: bool = True,
                  enable_normalization: bool = True, verbose: bool = False,
-                 strict: bool = False, require_gpu_inputs: bool = True):
+                 strict: bool = False, require_gpu_inputs: bool = True,
+                 enable_linear: bool = True):
         self.enable_attention = enable_attention
         self.enable_activation = enable_activation
         self.enable_normalization = enable_normalization
         self.verbose = verbose
         self.strict = strict
         self.require_gpu_inputs = require_gpu_inputs
+        self.enable_linear = enable_linear
         self.stats = OptimizationStats()
 
     def _groups(self):
@@ -80,6 +91,7 @@ class FXOptimizer:
             for pattern in sorted(group, key=lambda p: -p.priority):
                 if pattern.enabled:
                     self._apply_pattern(gm, pattern)
+        self._structural(gm)
         gm.graph.lint()
         gm.recompile()
         if self.verbose:
@@ -108,6 +120,73 @@ class FXOptimizer:
     def get_stats(self) -> OptimizationStats:
         return self.stats
 
+    # ------------------------------------------------- structural pass ---
+    def _structural(self, gm: torch.fx.GraphModule) -> None:
+        g = gm.graph
+        mods = dict(gm.named_modules())
+        count: dict[str, int] = {}
+
+        def bump(name):
+            count[name] = count.get(name, 0) + 1
+
+        def replace(node, fn, args):
+            with g.inserting_before(node):
+                new = g.call_function(fn, tuple(args))
+            new.meta.update(node.meta)
+            node.replace_all_uses_with(new)
+            g.erase_node(node)
+            return new
+
+        for node in list(g.nodes):
+            if node.graph is not g or node.op not in ("call_function", "call_module"):
+                continue
+            if self.enable_attention:
+                sd = _as_sdpa(node)
+                if sd is not None:
+                    replace(node, P.hip_attention, sd)
+                    bump("structural_sdpa_to_flash")
+                    continue
+            if self.enable_activation:
+                x = _as_gelu(node, mods)
+                if x is not None:
+                    lin = _as_linear(gm, x[0], mods) if len(x[0].users) == 1 else None
+                    if lin is not None and x[1] == "none":
+                        src = x[0]
+                        replace(node, P.hip_linear_gelu, lin)
+                        g.erase_node(src)
+                        bump("structural_linear_gelu")
+                    else:
+                        replace(node, P.hip_gelu_erf if x[1] == "none" else P.hip_gelu_tanh,
+                                [x[0]])
+                        bump("structural_gelu")
+                    continue
+            if self.enable_normalization:
+                ln = _as_layernorm(gm, node, mods)
+                if ln is not None:
+                    inp, w, b, eps = ln
+                    if (inp.op == "call_function" and inp.target in _ADD and len(inp.users) == 1
+                            and len(inp.args) == 2 and not inp.kwargs
+                            and all(isinstance(a, torch.fx.Node) for a in inp.args)):
+                        a0, a1 = inp.args
+                        replace(node, P.hip_add_layernorm_eps, [a0, a1, w, b, eps])
+                        g.erase_node(inp)
+                        bump("structural_add_layernorm")
+                    else:
+                        replace(node, P.hip_layernorm, [inp, w, b, eps])
+                        bump("structural_layernorm")
+                    continue
+            if self.enable_linear and not _feeds_gelu(node, mods):
+                lin = _as_linear(gm, node, mods)
+                if lin is not None:
+                    replace(node, P.hip_linear, lin)
+                    bump("structural_linear")
+                    continue
+        for name, n in count.items():
+            self.stats.patterns_matched += 1
+            self.stats.patterns_replaced += n
+            self.stats.passes_applied.append(name)
+        g.eliminate_dead_code()
+
 
 def optimize_fx_graph(gm: Any, example_inputs: Optional[list] = None, **kwargs) -> Any:
     """One-shot FXOptimizer(**kwargs).optimize(gm, example_inputs)."""
@@ -119,10 +198,101 @@ def is_fx_available() -> bool:
 
 
 def replaced_targets(gm: torch.fx.GraphModule) -> list[str]:
-    """Names of the HIP replacement functions a rewritten graph calls."""
-    names = {f.__name__ for f in (P.zenith_sdpa_replacement, P.zenith_gelu_replacement,
-                                  P.zenith_gelu_erf_replacement, P.zenith_linear_gelu_replacement,
-                                  P.zenith_layernorm_replacement,
-                                  P.zenith_add_layernorm_replacement)}
+    """Names of the HIP leaf functions a rewritten graph calls."""
+    leaves = {f.__name__ for f in (P.hip_flash_attention, P.hip_gelu_tanh, P.hip_gelu_erf,
+                                   P.hip_linear_gelu, P.hip_layernorm, P.hip_add_layernorm,
+                                   P.hip_add_layernorm_eps, P.hip_attention, P.hip_linear)}
     return [n.target.__name__ for n in gm.graph.nodes
-            if n.op == "call_function" and getattr(n.target, "__name__", None) in names]
+            if n.op == "call_function" and getattr(n.target, "__name__", None) in leaves]
+
+
+# ------------------------------------------------ structural matchers ----
+_LINEAR = {F.linear, torch._C._nn.linear}
+_GELU = {F.gelu, torch._C._nn.gelu}
+_LAYERNORM = {F.layer_norm, torch.layer_norm}
+_ADD = {operator.add, operator.iadd, torch.add}
+_HEAD_DIMS = (32, 64, 128)
+
+
+def _arg(node, i, name, default=None):
+    if len(node.args) > i:
+        return node.args[i]
+    return node.kwargs.get(name, default)
+
+
+def _param(gm, node, mod_name, attr):
+    """get_attr node for a submodule parameter, inserted before `node`."""
+    if getattr(gm.get_submodule(mod_name), attr) is None:
+        return None
+    with gm.graph.inserting_before(node):
+        return gm.graph.get_attr(f"{mod_name}.{attr}")
+
+
+def _as_linear(gm, node, mods):
+    """(x, W[N,K], b) of F.linear(x, W, b) or an nn.Linear call, else None."""
+    if node.op == "call_function" and node.target in _LINEAR:
+        return [_arg(node, 0, "input"), _arg(node, 1, "weight"), _arg(node, 2, "bias")]
+    if node.op == "call_module" and isinstance(mods.get(node.target), torch.nn.Linear):
+        return [node.args[0], _param(gm, node, node.target, "weight"),
+                _param(gm, node, node.target, "bias")]
+    return None
+
+
+def _as_gelu(node, mods):
+    """(input, approximate) of a GELU call, else None."""
+    if node.op == "call_function" and node.target in _GELU:
+        return node.args[0], _arg(node, 1, "approximate", "none")
+    if node.op == "call_module" and isinstance(mods.get(node.target), torch.nn.GELU):
+        return node.args[0], mods[node.target].approximate
+    return None
+
+
+def _as_layernorm(gm, node, mods):
+    """(input, gamma, beta, eps) of a LayerNorm over the last dimension with
+    an affine transform, else None."""
+    if node.op == "call_function" and node.target in _LAYERNORM:
+        shape = _arg(node, 1, "normalized_shape")
+        w, b = _arg(node, 2, "weight"), _arg(node, 3, "bias")
+        if not isinstance(shape, (tuple, list)) or len(shape) != 1 or w is None or b is None:
+            return None
+        return node.args[0], w, b, float(_arg(node, 4, "eps", 1e-5))
+    if node.op == "call_module" and isinstance(mods.get(node.target), torch.nn.LayerNorm):
+        m = mods[node.target]
+        if len(m.normalized_shape) != 1 or m.weight is None or m.bias is None:
+            return None
+        return (node.args[0], _param(gm, node, node.target, "weight"),
+                _param(gm, node, node.target, "bias"), float(m.eps))
+    return None
+
+
+def _meta_last_dim(node):
+    for key in ("val", "example_value", "tensor_meta"):
+        v = node.meta.get(key) if isinstance(node, torch.fx.Node) else None
+        shape = getattr(v, "shape", None)
+        if shape is not None and len(shape):
+            try:
+                return int(shape[-1])
+            except (TypeError, ValueError):
+                return None
+    return None
+
+
+def _as_sdpa(node):
+    """(q, k, v, scale) of an unmasked, non-causal, dropout-free
+    scaled_dot_product_attention, else None."""
+    if node.op != "call_function" or node.target is not F.scaled_dot_product_attention:
+        return None
+    q, k, v = node.args[:3]
+    if _arg(node, 3, "attn_mask") is not None or _arg(node, 5, "is_causal", False):
+        return None
+    if float(_arg(node, 4, "dropout_p", 0.0) or 0.0) != 0.0 or node.kwargs.get("enable_gqa"):
+        return None
+    d = _meta_last_dim(q)
+    if d is not None and d not in _HEAD_DIMS:
+        return None
+    return [q, k, v, node.kwargs.get("scale")]
+
+
+def _feeds_gelu(node, mods) -> bool:
+    """A Linear whose only user is a GELU is left for the Linear+GELU fusion."""
+    return len(node.users) == 1 and _as_gelu(next(iter(node.users)), mods) is not None

@@ -19,7 +19,7 @@ registry helpers (`get_attention_patterns`, `get_activation_patterns`,
     (Linear+GELU epilogue), LayerNorm of a residual sum (Add+LayerNorm), and
     the functional scaled_dot_product_attention call.
 
-The replacement functions are leaves for torch.fx (`torch.fx.wrap`), so a
+Each replacement calls one `hip_*` leaf registered with torch.fx.wrap, so a
 rewritten graph contains one call_function node per fused kernel.
 Replacements accept only CUDA tensors (the HIP kernels raise RuntimeError
 otherwise); the optimizer rewrites a graph only when its example inputs live
@@ -76,9 +76,14 @@ def sdpa_pattern(q, k, v):
 
 
 @torch.fx.wrap
-def zenith_sdpa_replacement(q, k, v):
-    """HIP flash attention, scale 1/sqrt(head_dim), non-causal."""
+def hip_flash_attention(q, k, v):
+    """Leaf call into the HIP flash-attention kernel (scale 1/sqrt(head_dim),
+    non-causal)."""
     return zenith_cuda.flash_attention(q, k, v)
+
+
+def zenith_sdpa_replacement(q, k, v):
+    return hip_flash_attention(q, k, v)
 
 
 def sdpa_call_pattern(q, k, v):
@@ -96,9 +101,13 @@ def gelu_tanh_pattern(x):
 
 
 @torch.fx.wrap
-def zenith_gelu_replacement(x):
-    """HIP tanh-GELU (the reference's `zenith_cuda.gelu` semantics)."""
+def hip_gelu_tanh(x):
+    """Leaf call into the HIP tanh-GELU (the reference `zenith_cuda.gelu`)."""
     return zenith_cuda.gelu(x, approximate="tanh")
+
+
+def zenith_gelu_replacement(x):
+    return hip_gelu_tanh(x)
 
 
 def gelu_erf_pattern(x):
@@ -107,8 +116,12 @@ def gelu_erf_pattern(x):
 
 
 @torch.fx.wrap
-def zenith_gelu_erf_replacement(x):
+def hip_gelu_erf(x):
     return zenith_cuda.gelu(x, approximate="none")
+
+
+def zenith_gelu_erf_replacement(x):
+    return hip_gelu_erf(x)
 
 
 def linear_gelu_pattern(x, w, b):
@@ -118,9 +131,13 @@ def linear_gelu_pattern(x, w, b):
 
 
 @torch.fx.wrap
-def zenith_linear_gelu_replacement(x, w, b):
+def hip_linear_gelu(x, w, b):
     """One MFMA GEMM with the bias + erf-GELU epilogue fused."""
     return zenith_cuda.linear(x, w, b, activation="gelu")
+
+
+def zenith_linear_gelu_replacement(x, w, b):
+    return hip_linear_gelu(x, w, b)
 
 
 # -------------------------------------------------------- normalisation ---
@@ -138,9 +155,13 @@ def _rows(x):
 
 
 @torch.fx.wrap
-def zenith_layernorm_replacement(x, weight, bias, eps=1e-5):
+def hip_layernorm(x, weight, bias, eps=1e-5):
     """HIP LayerNorm over the last dimension of any-rank input."""
     return zenith_cuda.layernorm(_rows(x), weight, bias, eps).view(x.shape)
+
+
+def zenith_layernorm_replacement(x, weight, bias, eps=1e-5):
+    return hip_layernorm(x, weight, bias, eps)
 
 
 def add_layernorm_pattern(x, residual, weight, bias):
@@ -150,8 +171,29 @@ def add_layernorm_pattern(x, residual, weight, bias):
 
 
 @torch.fx.wrap
-def zenith_add_layernorm_replacement(x, residual, weight, bias):
+def hip_add_layernorm(x, residual, weight, bias):
     return zenith_cuda.add_layernorm(_rows(x), _rows(residual), weight, bias, 1e-12).view(x.shape)
+
+
+def zenith_add_layernorm_replacement(x, residual, weight, bias):
+    return hip_add_layernorm(x, residual, weight, bias)
+
+
+# Leaves used by the optimizer's structural pass (module and functional
+# forms with explicit eps / scale).
+@torch.fx.wrap
+def hip_add_layernorm_eps(x, residual, weight, bias, eps):
+    return zenith_cuda.add_layernorm(_rows(x), _rows(residual), weight, bias, eps).view(x.shape)
+
+
+@torch.fx.wrap
+def hip_linear(x, w, b):
+    return zenith_cuda.linear(x, w, b)
+
+
+@torch.fx.wrap
+def hip_attention(q, k, v, scale):
+    return zenith_cuda.flash_attention(q, k, v, scale=scale)
 
 
 # ------------------------------------------------------------- registry ---
