@@ -1,28 +1,39 @@
 #!/usr/bin/env python3
 """Benchmark: BERT-base encoder seqs/s on one MI355X through the zenith_amd
-HIP kernels (BASELINE.json metric, config 5 at b32 s128 fp16).
+HIP kernels (BASELINE.json metric; config 5 at b32 s128 fp16 is `value`).
 
 One step = one forward of the 12-layer encoder over one batch of 32
 sequences x 128 tokens (synthetic, seeded; key-padding lengths ~ U{64..128}),
-replayed from a HIP graph, inputs resident in HBM. Prints ONE JSON line.
+replayed from a HIP graph, inputs resident in HBM. Prints ONE JSON line with:
 
-Also measured in the same run:
-  roofline  - the dominant kernel (FFN GEMM, 4096x768 -> 3072 with the fused
-              bias+GELU epilogue) timed with HIP events on its launch stream;
-              achieved = 2*M*N*K / average launch time vs the 2.5 PFLOP/s fp16
-              dense MFMA peak. `traffic` comes from the committed rocprofv3
-              PMC summary (profiles/gemm_ffn_up_pmc.json) when present.
-  cpu_baseline - the CPU oracle (numpy fp32 restatement of the reference's CPU
-              path) on a bounded sample of the same workload (whole sequences
-              of 128 tokens through 12 layers), on this host's cores.
-  int8      - the INT8-FFN variant of the same encoder (extra field).
+  value / ms_per_step  fp16 encoder (the INT8-FFN variant in `int8_ffn`)
+  roofline             the dominant kernel (FFN-up GEMM, 4096x768 -> 3072,
+                       bias + erf-GELU epilogue, 2*M*N*K = 19.33 GFLOP per
+                       launch) timed with HIP events on its launch stream;
+                       `traffic` from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+                       summary in profiles/gemm_ffn_up_pmc.md when present
+  kernels              per-kernel times and roofline fractions for the
+                       workload configs: FP16 GEMM sweep (config 2), flash
+                       attention s128 / s512 (config 3), INT8 FFN GEMMs
+                       (config 4), Add+LayerNorm and bias+GELU (HBM, buffer
+                       sets rotated past the 256 MB MALL)
+  cpu_baseline         the CPU oracle (numpy fp32 restatement of the
+                       reference's CPU path) on a bounded sample of the same
+                       workload (whole sequences through 12 layers)
+
+`--only NAME --iters N` launches one kernel N times and exits (for
+rocprofv3 counter runs); NAME is one of the `kernels` names or `copy`
+(a 256 MB fp16 read + 256 MB write, the calibration kernel for the
+FETCH_SIZE / WRITE_SIZE counters).
 """
 
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
+import re
 import sys
 import time
 
@@ -30,8 +41,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "BERT-base seqs/s (b32,s128,fp16/int8); GEMM & attn TFLOPS as % of MI355X peak"
-PEAK_FP16_TFLOPS = 2500.0
-PEAK_HBM_GBS = 8000.0
+PEAK = {"fp16": 2500.0, "int8": 5000.0, "hbm": 8000.0}  # TFLOP/s, TOP/s, GB/s
 
 
 def _args():
@@ -46,79 +56,211 @@ def _args():
                     help="bound on the CPU-baseline sample (whole sequences)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-int8", action="store_true")
+    ap.add_argument("--no-kernels", action="store_true")
+    ap.add_argument("--only", default=None, help="launch one kernel --iters times and exit")
+    ap.add_argument("--iters", type=int, default=20)
     return ap.parse_args()
 
 
-def time_kernel_events(torch, launch, n_iter=200, n_warm=20):
-    """Average duration of `launch()` (one kernel) over n_iter back-to-back
-    launches, bracketed by HIP events recorded on the launch stream."""
-    stream = torch.cuda.current_stream()
+# ------------------------------------------------------------------ timing --
+def time_launches(torch, launch, n_iter=50, n_warm=5):
+    """Average duration (s) of launch() over n_iter back-to-back launches,
+    bracketed by HIP events on the current stream (the stream every
+    zenith_amd launch goes to)."""
     for _ in range(n_warm):
-        launch()
+        launch(0)
+    stream = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record(stream)
-    for _ in range(n_iter):
-        launch()
+    for i in range(n_iter):
+        launch(i)
     e1.record(stream)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / 1e3 / n_iter  # seconds per launch
+    return e0.elapsed_time(e1) / 1e3 / n_iter
 
 
-def gemm_roofline(torch, dev):
+def _rc(L, rc):
+    if rc:
+        raise RuntimeError(L.last_error())
+
+
+# ----------------------------------------------------------- kernel cases --
+def kernel_cases(torch, dev):
+    """name -> (setup() -> (launch(i), work, unit, peak_key, bound, shape)).
+    `work` is the algorithmic FLOP / OP / byte count of one launch."""
     import numpy as np
 
     from zenith_amd import _lib as L
     from zenith_amd import synthetic
 
-    M, K, N = 4096, 768, 3072
-    a = torch.from_numpy(synthetic.normal((M, K), tag=1)).to(dev, torch.float16)
-    w = torch.from_numpy(synthetic.normal((N, K), tag=2, std=0.02)).to(dev, torch.float16)
-    b = torch.zeros(N, dtype=torch.float16, device=dev)
-    c = torch.empty((M, N), dtype=torch.float16, device=dev)
-    stream = torch.cuda.current_stream().cuda_stream
-    args = (a.data_ptr(), w.data_ptr(), c.data_ptr(), M, N, K, K, K, N, 1, L.ZK_F16,
-            b.data_ptr(), None, 0, L.ZK_EPI_BIAS_GELU_ERF, stream)
-    fn = L.load().zk_gemm_f16
+    lib = L.load()
+    s = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    f16 = torch.float16
 
-    def launch():
-        rc = fn(*args)
-        if rc:
-            raise RuntimeError(L.last_error())
+    def gemm(M, K, N, epi):
+        def setup():
+            a = torch.from_numpy(synthetic.uniform((M, K), tag=1)).to(dev, f16)
+            w = torch.from_numpy(synthetic.uniform((N, K), tag=2)).to(dev, f16) * 0.05
+            b = torch.zeros(N, dtype=f16, device=dev)
+            c = torch.empty((M, N), dtype=f16, device=dev)
+            st = s()
+            args = (a.data_ptr(), w.data_ptr(), c.data_ptr(), M, N, K, K, K, N, 1, L.ZK_F16,
+                    b.data_ptr(), None, 0, epi, st)
+            keep = (a, w, b, c)
+            return (lambda i: _rc(L, lib.zk_gemm_f16(*args)) and keep), 2.0 * M * N * K, \
+                "TFLOP/s", "fp16", "mfma", f"M={M} K={K} N={N}"
+        return setup
 
-    t = time_kernel_events(torch, launch)
-    flops = 2.0 * M * N * K
-    achieved = flops / t / 1e12
-    traffic = None
-    pmc = os.path.join(ROOT, "profiles", "gemm_ffn_up_pmc.json")
-    if os.path.exists(pmc):
-        try:
-            with open(pmc) as f:
-                traffic = json.load(f).get("hbm_bytes_per_launch")
-        except (OSError, ValueError):
-            traffic = None
+    def gemm_i8(M, K, N, epi):
+        def setup():
+            a = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev)
+            w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev)
+            sw = torch.full((N,), 1e-3, dtype=torch.float32, device=dev)
+            b = torch.zeros(N, dtype=f16, device=dev)
+            c = torch.empty((M, N), dtype=f16, device=dev)
+            args = (a.data_ptr(), w.data_ptr(), c.data_ptr(), M, N, K, K, K, N, 0.01,
+                    sw.data_ptr(), b.data_ptr(), None, 0, epi, L.ZK_F16, s())
+            keep = (a, w, sw, b, c)
+            return (lambda i: _rc(L, lib.zk_gemm_i8(*args)) and keep), 2.0 * M * N * K, \
+                "TOP/s", "int8", "mfma", f"M={M} K={K} N={N}"
+        return setup
+
+    def attn(S):
+        def setup():
+            B, H, D = 32, 12, 64
+            q, k, v = (torch.from_numpy(synthetic.normal((B, H, S, D), tag=50 + i))
+                       .to(dev, f16) for i in range(3))
+            o = torch.empty_like(q)
+            lens = torch.from_numpy(synthetic.padding_lengths(B, S)).to(dev)
+            strides = L.strides_arg([*q.stride()[:3], *k.stride()[:3], *v.stride()[:3],
+                                     *o.stride()[:3]])
+            args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), B, H, S, S, D,
+                    strides, lens.data_ptr(), 1.0 / math.sqrt(D), L.ZK_F16, s())
+            keep = (q, k, v, o, lens, strides)
+            return (lambda i: _rc(L, lib.zk_flash_attn_fwd(*args)) and keep), \
+                4.0 * B * H * S * S * D, "TFLOP/s", "fp16", "mfma", \
+                f"B={B} H={H} S={S} D={D} lens~U{{S/2..S}} (dense FLOPs)"
+        return setup
+
+    def add_ln():
+        def setup():
+            M, H = 4096, 768
+            per = 3 * M * H * 2
+            n = max(2, (512 << 20) // per + 1)  # rotate past the 256 MB MALL
+            xs = [torch.randn(M, H, device=dev, dtype=f16) for _ in range(n)]
+            rs = [torch.randn(M, H, device=dev, dtype=f16) for _ in range(n)]
+            ys = [torch.empty(M, H, device=dev, dtype=f16) for _ in range(n)]
+            g = torch.ones(H, device=dev, dtype=f16)
+            b = torch.zeros(H, device=dev, dtype=f16)
+            st = s()
+            keep = (xs, rs, ys, g, b)
+
+            def launch(i):
+                j = i % n
+                _rc(L, lib.zk_layernorm(xs[j].data_ptr(), rs[j].data_ptr(), g.data_ptr(),
+                                        b.data_ptr(), ys[j].data_ptr(), M, H, 1e-12, L.ZK_F16, st))
+                return keep
+            return launch, float(per), "GB/s", "hbm", "hbm", \
+                f"[{M},{H}] fp16, {n} rotating buffer sets"
+        return setup
+
+    def bias_gelu():
+        def setup():
+            M, N = 4096, 3072
+            per = 2 * M * N * 2
+            n = max(2, (512 << 20) // per + 1)
+            xs = [torch.randn(M, N, device=dev, dtype=f16) for _ in range(n)]
+            ys = [torch.empty(M, N, device=dev, dtype=f16) for _ in range(n)]
+            b = torch.randn(N, device=dev, dtype=f16)
+            st = s()
+            keep = (xs, ys, b)
+
+            def launch(i):
+                j = i % n
+                _rc(L, lib.zk_gelu(xs[j].data_ptr(), b.data_ptr(), ys[j].data_ptr(), M, N,
+                                   L.ZK_GELU_ERF, L.ZK_F16, st))
+                return keep
+            return launch, float(per), "GB/s", "hbm", "hbm", \
+                f"[{M},{N}] fp16 erf, {n} rotating buffer sets"
+        return setup
+
+    def copy():
+        def setup():
+            n = 128 << 20  # fp16 elements: 256 MB in, 256 MB out
+            x = torch.ones(n, device=dev, dtype=f16)
+            y = torch.empty_like(x)
+            st = s()
+            keep = (x, y)
+            return (lambda i: _rc(L, lib.zk_relu(x.data_ptr(), y.data_ptr(), n, L.ZK_F16, st))
+                    and keep), float(4 * n), "GB/s", "hbm", "hbm", "256 MB read + 256 MB write"
+        return setup
+
     del np
+    E = L.ZK_EPI_BIAS
     return {
-        "kernel": "gemm_mfma_kernel<F16,128x128,bias+gelu_erf> M=4096 N=3072 K=768",
-        "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
-        "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": traffic,
-        "avg_launch_us": round(t * 1e6, 3), "flops_per_launch": flops,
+        "gemm_qkv": gemm(4096, 768, 2304, E),
+        "gemm_out_proj": gemm(4096, 768, 768, E),
+        "gemm_ffn_up": gemm(4096, 768, 3072, L.ZK_EPI_BIAS_GELU_ERF),
+        "gemm_ffn_down": gemm(4096, 3072, 768, E),
+        "gemm_sq1024": gemm(1024, 1024, 1024, L.ZK_EPI_NONE),
+        "gemm_sq4096": gemm(4096, 4096, 4096, L.ZK_EPI_NONE),
+        "gemm_sq8192": gemm(8192, 8192, 8192, L.ZK_EPI_NONE),
+        "attn_s128": attn(128),
+        "attn_s512": attn(512),
+        "int8_ffn_up": gemm_i8(4096, 768, 3072, L.ZK_EPI_BIAS_GELU_ERF),
+        "int8_ffn_down": gemm_i8(4096, 3072, 768, E),
+        "add_layernorm": add_ln(),
+        "bias_gelu": bias_gelu(),
+        "copy": copy(),
     }
 
 
+def measure_kernels(torch, dev, names=None):
+    out = []
+    cases = kernel_cases(torch, dev)
+    for name, setup in cases.items():
+        if name == "copy" or (names and name not in names):
+            continue
+        launch, work, unit, peak_key, bound, shape = setup()
+        iters = 10 if "sq8192" in name else 50
+        t = time_launches(torch, launch, n_iter=iters)
+        scale = 1e12 if unit in ("TFLOP/s", "TOP/s") else 1e9
+        ach = work / t / scale
+        out.append({"name": name, "shape": shape, "us": round(t * 1e6, 3), "bound": bound,
+                    "achieved": round(ach, 2), "unit": unit, "peak": PEAK[peak_key],
+                    "frac": round(ach / PEAK[peak_key], 4)})
+        del launch
+        torch.cuda.empty_cache()
+    return out
+
+
+def pmc_traffic():
+    """HBM bytes per launch of the FFN-up GEMM from the committed rocprofv3
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel
+    calibration); None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "gemm_ffn_up_pmc.md")
+    try:
+        txt = open(path).read()
+    except OSError:
+        return None
+    m = re.search(r"hbm_bytes_per_launch:\s*([0-9.eE+]+)", txt)
+    return float(m.group(1)) if m else None
+
+
+# ---------------------------------------------------------- CPU baseline --
 def cpu_baseline(seq: int, layers: int, budget_s: float):
     """Oracle fp32 encoder on whole sequences until the time budget is used."""
-    import numpy as np
-
     from oracle import bert as obert
     from zenith_amd import synthetic
 
     try:
         from threadpoolctl import threadpool_info
 
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-        blas = ",".join(sorted({i.get("internal_api", "?") for i in threadpool_info()}))
+        info = threadpool_info()
+        threads = max([i.get("num_threads", 1) for i in info] or [1])
+        blas = ",".join(sorted({i.get("internal_api", "?") for i in info}))
     except Exception:  # pragma: no cover
         threads, blas = int(os.environ.get("OMP_NUM_THREADS", "1")), "unknown"
     w = synthetic.bert_weights(layers, seed=42)
@@ -136,8 +278,27 @@ def cpu_baseline(seq: int, layers: int, budget_s: float):
     return {
         "value": round(done / el, 4), "unit": "seqs/s", "cores": int(threads), "kind": "port",
         "sample": f"{done} sequences x {seq} tokens through {layers} fp32 layers "
-                  f"(numpy oracle, {blas} BLAS), {el:.1f} s; host cpus={len(os.sched_getaffinity(0))}",
+                  f"(numpy oracle, {blas} BLAS, {threads} threads), {el:.1f} s; "
+                  f"host cpus={len(os.sched_getaffinity(0))}",
     }
+
+
+def _calibrate(enc, x, lens, torch):
+    """absmax/127 of the FFN-up input (h1) and GELU output (u) per layer from
+    one eager fp16 pass (MinMax rule, zenith/optimization/quantization.py:101-107)."""
+    B, S, H = x.shape
+    enc._buffers(B, S)
+    bf = enc._bufs
+    stream = torch.cuda.current_stream().cuda_stream
+    cur = x.reshape(B * S, H).contiguous()
+    s_x, s_h = [], []
+    for i in range(len(enc.layers)):
+        out = torch.empty_like(cur)
+        enc._layer(i, cur, out, lens, B, S, stream)
+        s_x.append(max(float(bf["h1"].abs().max()) / 127.0, 1e-8))
+        s_h.append(max(float(bf["u"].abs().max()) / 127.0, 1e-8))
+        cur = out
+    return s_x, s_h
 
 
 def main():
@@ -146,7 +307,6 @@ def main():
         print("bench.py: this build measures one GPU only (the encoder shards by batch; "
               "multi-GPU runs are not part of it). Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
-    import numpy as np
     import torch
 
     from zenith_amd import synthetic
@@ -156,6 +316,19 @@ def main():
         print("bench.py: no GPU available", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+
+    if args.only:
+        cases = kernel_cases(torch, dev)
+        if args.only not in cases:
+            print(f"bench.py: --only must be one of {sorted(cases)}", file=sys.stderr)
+            sys.exit(2)
+        launch = cases[args.only]()[0]
+        for i in range(args.iters):
+            launch(i)
+        torch.cuda.synchronize()
+        print(f"bench.py: {args.only} x {args.iters} done", flush=True)
+        return
+
     B, S = args.batch, args.seq
     layers = synthetic.bert_weights(args.layers, seed=42)
     enc = BertEncoder(layers, device=dev)
@@ -177,22 +350,24 @@ def main():
 
     dt = timed(args.steps, args.warmup)
     seqs_s = B * args.steps / dt
-    out = go.float()
-    assert torch.isfinite(out).all(), "non-finite encoder output"
+    assert torch.isfinite(go.float()).all(), "non-finite encoder output"
 
     int8 = None
     if not args.no_int8:
-        # per-layer activation scales from one fp16 calibration pass
         s_x, s_h = _calibrate(enc, x, lens, torch)
         enc.enable_int8_ffn(s_x, s_h, layers_fp32=layers)
         enc.capture(B, S)
         enc._gx.copy_(x)
         enc._gl.copy_(lens)
         dt8 = timed(args.steps, args.warmup)
-        int8 = {"value": round(B * args.steps / dt8, 2), "ms_per_step": round(dt8 / args.steps * 1e3, 4)}
+        int8 = {"value": round(B * args.steps / dt8, 2),
+                "ms_per_step": round(dt8 / args.steps * 1e3, 4)}
         enc.disable_int8_ffn()
+    del enc
+    torch.cuda.empty_cache()
 
-    roof = gemm_roofline(torch, dev)
+    roof = measure_kernels(torch, dev, ["gemm_ffn_up"])[0]
+    kernels = None if args.no_kernels else measure_kernels(torch, dev)
     cpu = None if args.no_cpu else cpu_baseline(S, args.layers, args.cpu_seconds)
     fwd_flops = args.layers * (2 * B * S * 768 * (3 * 768 + 768 + 2 * 3072) + 4 * B * 12 * S * S * 64)
     line = {
@@ -205,32 +380,14 @@ def main():
                    "global_batch": B, "seq_len": S, "parallelism": "none (1 GPU)"},
         "encoder_tflops": round(fwd_flops * args.steps / dt / 1e12, 2),
         "int8_ffn": int8,
-        "roofline": {k: roof[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
-        "roofline_kernel": {k: roof[k] for k in ("kernel", "avg_launch_us", "flops_per_launch")},
+        "roofline": {"bound": "mfma", "achieved": roof["achieved"], "peak": roof["peak"],
+                     "unit": roof["unit"], "frac": roof["frac"], "traffic": pmc_traffic()},
+        "roofline_kernel": {"kernel": "gemm_mfma_kernel<F16, bias+gelu_erf> M=4096 K=768 N=3072",
+                            "avg_launch_us": roof["us"], "flops_per_launch": 2.0 * 4096 * 768 * 3072},
+        "kernels": kernels,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
-
-
-def _calibrate(enc, x, lens, torch):
-    """absmax/127 of the FFN-up input (h1) and GELU output (u) per layer from
-    one eager fp16 pass (MinMax rule, zenith/optimization/quantization.py:101-107)."""
-    from zenith_amd import _lib as L
-
-    B, S, H = x.shape
-    enc._buffers(B, S)
-    bf = enc._bufs
-    stream = torch.cuda.current_stream().cuda_stream
-    cur = x.reshape(B * S, H).contiguous()
-    s_x, s_h = [], []
-    for i in range(len(enc.layers)):
-        out = torch.empty_like(cur)
-        enc._layer(i, cur, out, lens, B, S, stream)
-        s_x.append(max(float(bf["h1"].abs().max()) / 127.0, 1e-8))
-        s_h.append(max(float(bf["u"].abs().max()) / 127.0, 1e-8))
-        cur = out
-    del L
-    return s_x, s_h
 
 
 if __name__ == "__main__":
