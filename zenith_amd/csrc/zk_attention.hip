@@ -80,8 +80,8 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
       const int kk = t * KT + idx / DV;  // K: 16-byte vectors row-contiguous
       kr[v] = kk < p.Sk ? *(const f16x8 *)(Kb + kk * p.sk[2] + (idx % DV) * 8)
                         : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      const int kv = t * KT + idx % KT;  // V: one key per lane (transposed store)
-      vr[v] = kv < p.Sk ? *(const f16x8 *)(Vb + kv * p.sv[2] + (idx / KT) * 8)
+      // V like K (8 lanes per 128-byte row, coalesced); transposed when stored.
+      vr[v] = kk < p.Sk ? *(const f16x8 *)(Vb + kk * p.sv[2] + (idx % DV) * 8)
                         : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
     }
   };
@@ -90,7 +90,7 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
     for (int v = 0; v < PER; ++v) {
       const int idx = tid + v * NT;
       *(f16x8 *)(Ks + (idx / DV) * KLD + (idx % DV) * 8) = kr[v];
-      const int key = idx % KT, d0 = (idx / KT) * 8;
+      const int key = idx / DV, d0 = (idx % DV) * 8;
 #pragma unroll
       for (int j = 0; j < 8; ++j) Vt[(d0 + j) * VLD + key] = vr[v][j];
     }
@@ -115,37 +115,50 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
         s[kb] = mfma32x32x16(kf, qf[c], s[kb]);
       }
     }
-    // Scale into the log2 domain, mask, tile max.
+    // Tile max on the raw scores (the scale is positive), masking only the
+    // tile that straddles the valid length.
+    const bool partial = t * KT + KT > L;
+    if (partial) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = t * KT + kb * 32 + 8 * (r >> 2) + 4 * h32 + (r & 3);
+          if (key >= L) s[kb][r] = -__builtin_inff();
+        }
+    }
     float tmax = -__builtin_inff();
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = t * KT + kb * 32 + 8 * (r >> 2) + 4 * h32 + (r & 3);
-        const float v = key < L ? s[kb][r] * p.scale_log2 : -__builtin_inff();
-        s[kb][r] = v;
-        tmax = fmaxf(tmax, v);
-      }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m, tmax);  // finite: key t*KT < L is valid
-    const float alpha = exp2f(m - m_new);
-    m = m_new;
+      for (int r = 0; r < 16; r += 2) tmax = fmaxf(tmax, fmaxf(s[kb][r], s[kb][r + 1]));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * p.scale_log2;  // finite: key t*KT < L
+    // Lazy rescaling: the reference point m (log2 units) only moves when the
+    // tile max exceeds it by more than 8, so exp2(s - m) <= 256 always fits
+    // fp16 and the accumulator is rescaled on a few tiles only. O / l is
+    // independent of the reference point, so this is exact.
+    if (__builtin_amdgcn_ballot_w64(tmax > m + 8.0f) != 0) {
+      const float m_new = fmaxf(m, tmax);
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 on the first tile
+      m = m_new;
+      l *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+    }
     float psum = 0.f;
     f16x8 pf[2][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float e = exp2f(s[kb][r] - m);
+        const float e = __builtin_amdgcn_exp2f(fmaf(s[kb][r], p.scale_log2, -m));
         psum += e;
         pf[kb][r >> 3][r & 7] = (f16)e;
       }
     psum += __shfl_xor(psum, 32, 64);
-    l = l * alpha + psum;
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+    l += psum;
     // O^T[d][q] += V^T[d][key] . P^T[key][q], 16 keys per MFMA. Lane-half
     // h32, slot j of the P^T fragment holds key 16*c2 + 8*(j/4) + 4*h32 +
     // j%4 of block kb; the V^T fragment is read with the same key order.
@@ -247,8 +260,9 @@ __global__ __launch_bounds__(256) void fa_fwd_f32_kernel(AttnParams p) {
 
 template <int D>
 static void launch_f16(const AttnParams &p, hipStream_t s) {
-  const int64_t blocks128 = (int64_t)p.B * p.H * ((p.Sq + 127) / 128);
-  if (blocks128 >= 1024) {
+  // 4 wavefronts x 32 queries per workgroup: at seq 128 one workgroup holds a
+  // whole (batch, head), so K and V are read from HBM once.
+  if (p.Sq >= 128) {
     dim3 grid((unsigned)((p.Sq + 127) / 128), (unsigned)p.H, (unsigned)p.B);
     fa_fwd_f16_kernel<D, 4><<<grid, 256, 0, s>>>(p);
   } else {

@@ -7,8 +7,9 @@
 //
 // Workgroup: 4 wavefronts in a 2 x 2 grid, each owning a (BM/2) x (BN/2)
 // wave tile made of MS x MS MFMA blocks (MS = 32 or 16). The macro tile is
-// chosen per shape so that the BERT projections fill the 256 CUs in one
-// round (e.g. 256 x 192 tiles give exactly 256 tiles for M=4096, N=3072).
+// chosen per shape from measurements (pick_cfg); small tiles with several
+// workgroups per CU win at the BERT projection shapes, where a K of 768
+// leaves too few slices to amortise a deep pipeline.
 //
 // K is walked in slices of BKB bytes per row. A slice of A and W goes from
 // global memory straight into LDS with buffer_load ... lds (16 bytes per
@@ -218,8 +219,14 @@ __device__ __forceinline__ void interleave() {
   }
 }
 
+// Two workgroups per CU (two waves per SIMD) whenever the LDS ring allows
+// it; the register budget then has to fit 256 per lane.
+constexpr int gemm_waves_per_eu(int smem_bytes) { return smem_bytes <= 80 * 1024 ? 2 : 1; }
+
 template <class OP, int BM, int BN, int MS, int BKB, int ST, int EPI, typename OutT, bool DEQ>
-__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(gemm_waves_per_eu(GemmCfg<OP, BM, BN, MS, BKB, ST>::SMEM))))
+void gemm_mfma_kernel(GemmParams p) {
   typedef GemmCfg<OP, BM, BN, MS, BKB, ST> G;
   typedef typename OP::template Mma<MS> MM;
   typedef typename OP::Frag Frag;
@@ -322,40 +329,42 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
 #else
 #define ZK_ISSUE(kt, stage) ((void)(kt), (void)(stage))
 #endif
-  // Prologue: one slice per stage.
+  {
+    // Prologue: one slice per stage.
 #pragma unroll
-  for (int s = 0; s < ST; ++s)
-    if (s < nk) ZK_ISSUE(s, s);
-  wait_slices<ST - 1, IA + IB>(nk - 1);
-  lds_barrier();
-  rd(0, 0, 0);
-  // Main loop over slices. Before the last k-step of slice kt every wave
-  // waits for slice kt + 1 and meets at the barrier; by then the ring stage
-  // of slice kt has been read completely (its last fragments are in
-  // registers), so slice kt + ST is issued into it, and the first
-  // fragments of slice kt + 1 are read under the last MFMAs of slice kt.
-  auto steps_but_last = [&](int stage) {
-#pragma unroll
-    for (int ks = 0; ks + 1 < KS; ++ks) {
-      rd(stage, ks + 1, (ks + 1) & 1);
-      mma_step(ks & 1);
-      interleave<TM + TN, TM * TN>();
-    }
-  };
-  int stage = 0;
-  for (int kt = 0; kt + 1 < nk; ++kt) {
-    steps_but_last(stage);
-    const int next = stage + 1 == ST ? 0 : stage + 1;
-    wait_slices<ST - 2, IA + IB>(nk - 2 - kt);
+    for (int s = 0; s < ST; ++s)
+      if (s < nk) ZK_ISSUE(s, s);
+    wait_slices<ST - 1, IA + IB>(nk - 1);
     lds_barrier();
-    if (kt + ST < nk) ZK_ISSUE(kt + ST, stage);
-    rd(next, 0, 0);
+    rd(0, 0, 0);
+    // Main loop over slices. Before the last k-step of slice kt every wave
+    // waits for slice kt + 1 and meets at the barrier; by then the ring stage
+    // of slice kt has been read completely (its last fragments are in
+    // registers), so slice kt + ST is issued into it, and the first
+    // fragments of slice kt + 1 are read under the last MFMAs of slice kt.
+    auto steps_but_last = [&](int stage) {
+#pragma unroll
+      for (int ks = 0; ks + 1 < KS; ++ks) {
+        rd(stage, ks + 1, (ks + 1) & 1);
+        mma_step(ks & 1);
+        interleave<TM + TN, TM * TN>();
+      }
+    };
+    int stage = 0;
+    for (int kt = 0; kt + 1 < nk; ++kt) {
+      steps_but_last(stage);
+      const int next = stage + 1 == ST ? 0 : stage + 1;
+      wait_slices<ST - 2, IA + IB>(nk - 2 - kt);
+      lds_barrier();
+      if (kt + ST < nk) ZK_ISSUE(kt + ST, stage);
+      rd(next, 0, 0);
+      mma_step(1);
+      interleave<TM + TN, TM * TN>();
+      stage = next;
+    }
+    steps_but_last(stage);  // last slice: nothing left to prefetch
     mma_step(1);
-    interleave<TM + TN, TM * TN>();
-    stage = next;
   }
-  steps_but_last(stage);  // last slice: nothing left to prefetch
-  mma_step(1);
 #undef ZK_ISSUE
   __syncthreads();  // every wave is done reading the ring; it becomes epilogue space
 
@@ -445,13 +454,12 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
 }
 
 // ------------------------------------------------------------ dispatch ----
-// Tile configurations (BM, BN, MS, BKB, ST); measured on MI355X at the BERT
-// projection shapes and at squares (the choice rule is in pick_cfg).
-//   0: 256x256, 32x32 MFMA, 64-byte slices, 4 stages (128 KB ring, 1 WG/CU)
-//   1: 128x128, 32x32, 128-byte slices, 2 stages (64 KB)
-//   2: 128x96,  16x16, 128-byte slices, 2 stages (56 KB)
-//   3: 64x64,   16x16, 128-byte slices, 2 stages (32 KB, up to 5 WG/CU)
-//   4: 128x96,  16x16, 128-byte slices, 4 stages (112 KB)
+// Tile configurations (BM, BN, MS, BKB, ST); the choice rule is in pick_cfg.
+//   0: 256x256, 32x32 MFMA, 64-byte slices, 4-stage ring (1 WG/CU)
+//   1: 128x128, 32x32, 128-byte slices, 2-stage ring (2 WG/CU)
+//   2: 128x96,  16x16, 128-byte slices, 2-stage ring (2 WG/CU)
+//   3: 64x64,   16x16, 128-byte slices, 2-stage ring (up to 5 WG/CU)
+//   4: 128x128, 32x32, 128-byte slices, 3-stage ring (1 WG/CU)
 constexpr int kNumCfgs = 5;
 
 template <class OP, int BM, int BN, int MS, int BKB, int ST, typename OutT, bool DEQ>
@@ -477,9 +485,9 @@ static void launch_epi(GemmParams p, int epi, hipStream_t s) {
 #undef ZK_L
 }
 
-// Shape -> configuration, from measurements at M = 4096:
-//   N <= 1024 (out-projection, FFN-down): many small tiles keep every CU
-//     busy; 64x64 for short K, the deep-ring 128x96 for K >= 2048;
+// Shape -> configuration, from measurements at M = 4096 (bench.py kernels):
+//   N <= 1024 (out-projection, FFN-down): 64x64 tiles for short K keep every
+//     CU busy; for K >= 2048 the 3-stage 128x128 ring hides more latency;
 //   N >= 2048: 128x128 once that gives >= 640 tiles (FFN-up), else 128x96
 //     (QKV); very large problems take 256x256.
 // ZK_GEMM_CFG=<id> forces a configuration (tuning runs).
@@ -503,7 +511,7 @@ static void launch_mfma(GemmParams p, int epi, hipStream_t s) {
     case 0: launch_epi<OP, 256, 256, 32, 64, 4, OutT, DEQ>(p, epi, s); break;
     case 1: launch_epi<OP, 128, 128, 32, 128, 2, OutT, DEQ>(p, epi, s); break;
     case 2: launch_epi<OP, 128, 96, 16, 128, 2, OutT, DEQ>(p, epi, s); break;
-    case 4: launch_epi<OP, 128, 96, 16, 128, 4, OutT, DEQ>(p, epi, s); break;
+    case 4: launch_epi<OP, 128, 128, 32, 128, 3, OutT, DEQ>(p, epi, s); break;
     default: launch_epi<OP, 64, 64, 16, 128, 2, OutT, DEQ>(p, epi, s); break;
   }
 }

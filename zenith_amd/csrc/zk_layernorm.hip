@@ -1,7 +1,7 @@
 // LayerNorm and fused Add+LayerNorm (post-LN BERT residual), fp32 statistics.
 //
-// Fast path: one wavefront per row. Each lane keeps its slice of the row in
-// registers as 16-byte vectors, so the row is read from HBM exactly once
+// Fast path: one or two rows per wavefront. Each lane keeps its slice of the
+// row in registers as 16-byte vectors, so the row is read from HBM exactly once
 // (twice with the residual) and written once; mean and variance are exact
 // two-pass statistics over the register copy, reduced with cross-lane
 // butterflies. Rows whose hidden size is not a multiple of the vector width
@@ -15,28 +15,34 @@ template <typename T> struct LnVec;
 template <> struct LnVec<f16> { typedef f16x8 type; static constexpr int n = 8; };
 template <> struct LnVec<float> { typedef f32x4 type; static constexpr int n = 4; };
 
-constexpr int kLnWaves = 4;  // rows per 256-thread block
+constexpr int kLnWaves = 4;  // wavefronts per 256-thread block
 
-template <typename T, int MAXV, bool RES>
+// LPR lanes per row (64 / LPR rows per wavefront): a 768-wide fp16 row is 96
+// 16-byte vectors, so two rows per wavefront give every lane exactly three.
+template <typename T, int MAXV, bool RES, int LPR>
 __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
     const T *__restrict__ x, const T *__restrict__ res,
     const T *__restrict__ gamma, const T *__restrict__ beta, T *__restrict__ y,
     int64_t rows, int hidden, float eps) {
   typedef typename LnVec<T>::type V;
   constexpr int W = LnVec<T>::n;
+  constexpr int RPW = kWave / LPR;  // rows per wavefront
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = (int64_t)blockIdx.x * kLnWaves + (threadIdx.x >> 6);
-  if (row >= rows) return;  // whole wave exits together
+  const int sub = lane % LPR;
+  const int64_t row = ((int64_t)blockIdx.x * kLnWaves + (threadIdx.x >> 6)) * RPW + lane / LPR;
+  // Rows past the end load nothing and store nothing, but stay in the
+  // shuffles (their partner lanes belong to the same row group).
+  const bool live = row < rows;
   const int nvec = hidden / W;
-  const V *xr = reinterpret_cast<const V *>(x + row * hidden);
-  const V *rr = reinterpret_cast<const V *>(res + (RES ? row * hidden : 0));
+  const V *xr = reinterpret_cast<const V *>(x + (live ? row : 0) * hidden);
+  const V *rr = reinterpret_cast<const V *>(res + (RES && live ? row * hidden : 0));
 
   float v[MAXV][W];
   float sum = 0.f;
 #pragma unroll
   for (int k = 0; k < MAXV; ++k) {
-    const int idx = lane + k * kWave;
-    if (idx < nvec) {
+    const int idx = sub + k * LPR;
+    if (live && idx < nvec) {
       V a = xr[idx];
       V r;
       if (RES) r = rr[idx];
@@ -52,12 +58,17 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
       for (int j = 0; j < W; ++j) v[k][j] = 0.f;
     }
   }
+  auto group_sum = [](float t) {
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) t += __shfl_xor(t, o, kWave);
+    return t;
+  };
   const float inv_h = 1.0f / (float)hidden;
-  const float mean = wave_sum(sum) * inv_h;
+  const float mean = group_sum(sum) * inv_h;
   float sq = 0.f;
 #pragma unroll
   for (int k = 0; k < MAXV; ++k) {
-    if (lane + k * kWave < nvec) {
+    if (sub + k * LPR < nvec) {
 #pragma unroll
       for (int j = 0; j < W; ++j) {
         const float d = v[k][j] - mean;
@@ -65,15 +76,16 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
       }
     }
   }
-  const float var = wave_sum(sq) * inv_h;
+  const float var = group_sum(sq) * inv_h;
   const float rstd = 1.0f / sqrtf(var + eps);
+  if (!live) return;
 
   V *yr = reinterpret_cast<V *>(y + row * hidden);
   const V *gv = reinterpret_cast<const V *>(gamma);
   const V *bv = reinterpret_cast<const V *>(beta);
 #pragma unroll
   for (int k = 0; k < MAXV; ++k) {
-    const int idx = lane + k * kWave;
+    const int idx = sub + k * LPR;
     if (idx < nvec) {
       V g = gv[idx], b = bv[idx], o;
 #pragma unroll
@@ -124,14 +136,15 @@ __global__ __launch_bounds__(256) void ln_block_kernel(
   }
 }
 
-template <typename T, int MAXV>
+template <typename T, int MAXV, int LPR>
 static void ln_wave_launch(const T *x, const T *r, const T *g, const T *b, T *y,
                            int64_t rows, int hidden, float eps, hipStream_t s) {
-  const unsigned grid = (unsigned)((rows + kLnWaves - 1) / kLnWaves);
+  constexpr int rows_per_block = kLnWaves * (kWave / LPR);
+  const unsigned grid = (unsigned)((rows + rows_per_block - 1) / rows_per_block);
   if (r)
-    ln_wave_kernel<T, MAXV, true><<<grid, kLnWaves * kWave, 0, s>>>(x, r, g, b, y, rows, hidden, eps);
+    ln_wave_kernel<T, MAXV, true, LPR><<<grid, kLnWaves * kWave, 0, s>>>(x, r, g, b, y, rows, hidden, eps);
   else
-    ln_wave_kernel<T, MAXV, false><<<grid, kLnWaves * kWave, 0, s>>>(x, r, g, b, y, rows, hidden, eps);
+    ln_wave_kernel<T, MAXV, false, LPR><<<grid, kLnWaves * kWave, 0, s>>>(x, r, g, b, y, rows, hidden, eps);
 }
 
 template <typename T>
@@ -145,15 +158,17 @@ static int ln_impl(const void *xv, const void *rv, const void *gv,
   const bool vec_ok = hidden % W == 0 && aligned16(x) && aligned16(y) &&
                       aligned16(g) && aligned16(b) && (!r || aligned16(r));
   const int64_t nvec = hidden / W;
-  const int64_t per_lane = (nvec + kWave - 1) / kWave;
-  if (vec_ok && per_lane <= 16 && (rows + kLnWaves - 1) / kLnWaves <= 0x7fffffff) {
+  if (vec_ok && nvec <= 16 * kWave && (rows + kLnWaves - 1) / kLnWaves <= 0x7fffffff) {
     const int h = (int)hidden;
-    if (per_lane <= 1) ln_wave_launch<T, 1>(x, r, g, b, y, rows, h, eps, s);
-    else if (per_lane <= 2) ln_wave_launch<T, 2>(x, r, g, b, y, rows, h, eps, s);
-    else if (per_lane <= 3) ln_wave_launch<T, 3>(x, r, g, b, y, rows, h, eps, s);
-    else if (per_lane <= 4) ln_wave_launch<T, 4>(x, r, g, b, y, rows, h, eps, s);
-    else if (per_lane <= 8) ln_wave_launch<T, 8>(x, r, g, b, y, rows, h, eps, s);
-    else ln_wave_launch<T, 16>(x, r, g, b, y, rows, h, eps, s);
+    // 32 lanes per row while a row fits in 4 vectors per lane (H <= 1024 in
+    // fp16), else a whole wavefront per row.
+    if (nvec <= 32) ln_wave_launch<T, 1, 32>(x, r, g, b, y, rows, h, eps, s);
+    else if (nvec <= 64) ln_wave_launch<T, 2, 32>(x, r, g, b, y, rows, h, eps, s);
+    else if (nvec <= 96) ln_wave_launch<T, 3, 32>(x, r, g, b, y, rows, h, eps, s);
+    else if (nvec <= 128) ln_wave_launch<T, 4, 32>(x, r, g, b, y, rows, h, eps, s);
+    else if (nvec <= 256) ln_wave_launch<T, 4, 64>(x, r, g, b, y, rows, h, eps, s);
+    else if (nvec <= 512) ln_wave_launch<T, 8, 64>(x, r, g, b, y, rows, h, eps, s);
+    else ln_wave_launch<T, 16, 64>(x, r, g, b, y, rows, h, eps, s);
   } else {
     if (rows > 0x7fffffff)
       return fail(ZK_ERR_UNSUPPORTED, "zk_layernorm: too many rows for the generic path");
