@@ -87,6 +87,37 @@ def test_linear_epilogues(dev, act, M, K, N):
     assert ok, worst
 
 
+@pytest.mark.parametrize("M,K,N", [
+    (4100, 72, 4100),   # 8-wave 256x256 tile, ragged M / N / K, scalar stores
+    (4000, 100, 2000),  # 8-wave 256x192 tile, vector stores
+    (520, 200, 20500),  # 128x128, 2-stage ring
+    (700, 136, 1100),   # 128x96, 16x16 MFMA
+    (1000, 3000, 600),  # 128x128, 3-stage ring (long K)
+    (333, 500, 1000),   # 64x64, 16x16 MFMA
+])
+def test_linear_tile_configs(dev, M, K, N):
+    """Every tile configuration of the shape-driven choice, at ragged edges,
+    with the bias + residual epilogue."""
+    from zenith_amd import zenith_cuda as zc
+
+    x = synthetic.round_f16(synthetic.normal((M, K), tag=16))
+    w = synthetic.round_f16(synthetic.normal((N, K), tag=17, std=0.05))
+    b = synthetic.round_f16(synthetic.normal((N,), tag=18, std=0.5))
+    r = synthetic.round_f16(synthetic.normal((M, N), tag=19))
+    y = zc.linear(_t(x, dev, torch.float16), _t(w, dev, torch.float16), _t(b, dev, torch.float16),
+                  residual=_t(r, dev, torch.float16))
+    rows = np.random.default_rng(M).choice(M, min(M, 256), replace=False)
+    rows.sort()
+    ref = ops.matmul_f64(x[rows], w.T) + b + r[rows]
+    got = y[torch.from_numpy(rows).to(dev)].float().cpu().numpy()
+    ok, worst = fp16_tol(got, ref)
+    assert ok, worst
+    # edge rows and columns in full
+    last = ops.matmul_f64(x[-3:], w.T) + b + r[-3:]
+    ok, worst = fp16_tol(y[-3:].float().cpu().numpy(), last)
+    assert ok, worst
+
+
 def test_linear_3d_and_no_bias(dev):
     from zenith_amd import zenith_cuda as zc
 

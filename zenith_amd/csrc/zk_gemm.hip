@@ -5,11 +5,12 @@
 // step (32x32x16 or 16x16x32) and an int8 step (32x32x32 or 16x16x64) read
 // the same 16 bytes per lane and operand, so one LDS layout serves both.
 //
-// Workgroup: 4 wavefronts in a 2 x 2 grid, each owning a (BM/2) x (BN/2)
-// wave tile made of MS x MS MFMA blocks (MS = 32 or 16). The macro tile is
-// chosen per shape from measurements (pick_cfg); small tiles with several
-// workgroups per CU win at the BERT projection shapes, where a K of 768
-// leaves too few slices to amortise a deep pipeline.
+// Workgroup: 4 wavefronts in a 2 x 2 grid or 8 in a 2 x 4 / 4 x 2 grid,
+// each owning a (BM/WM) x (BN/WN) wave tile made of MS x MS MFMA blocks
+// (MS = 32 or 16). The macro tile is chosen per shape from measurements
+// (pick_cfg): 8-wave 256-row tiles (two waves of one workgroup per SIMD)
+// where the grid still fills the chip, small tiles with several workgroups
+// per CU for the narrow projections.
 //
 // K is walked in slices of BKB bytes per row. A slice of A and W goes from
 // global memory straight into LDS with buffer_load ... lds (16 bytes per
@@ -148,10 +149,10 @@ constexpr int epi_pitch16(int w) {
   return p;
 }
 
-template <class OP, int BM, int BN, int MS, int BKB, int ST>
+template <class OP, int BM, int BN, int MS, int BKB, int ST, int WM = 2, int WN = 2>
 struct GemmCfg {
-  static constexpr int NW = 4, NT = 256;
-  static constexpr int WTM = BM / 2, WTN = BN / 2;
+  static constexpr int NW = WM * WN, NT = 64 * NW;
+  static constexpr int WTM = BM / WM, WTN = BN / WN;
   static constexpr int TM = WTM / MS, TN = WTN / MS;
   static constexpr int CH = BKB / 16;          // 16-byte chunks per LDS row
   static constexpr int RPI = 1024 / BKB;       // rows per wavefront DMA instruction
@@ -219,15 +220,19 @@ __device__ __forceinline__ void interleave() {
   }
 }
 
-// Two workgroups per CU (two waves per SIMD) whenever the LDS ring allows
-// it; the register budget then has to fit 256 per lane.
-constexpr int gemm_waves_per_eu(int smem_bytes) { return smem_bytes <= 80 * 1024 ? 2 : 1; }
+// Waves per SIMD the register allocation must allow: as many workgroups
+// per CU as the LDS ring admits (NW / 4 waves per SIMD each), capped at 3.
+constexpr int gemm_waves_per_eu(int smem_bytes, int nw) {
+  return nw == 8 ? 2 : smem_bytes <= 53 * 1024 ? 3 : smem_bytes <= 80 * 1024 ? 2 : 1;
+}
 
-template <class OP, int BM, int BN, int MS, int BKB, int ST, int EPI, typename OutT, bool DEQ>
-__global__ __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu(gemm_waves_per_eu(GemmCfg<OP, BM, BN, MS, BKB, ST>::SMEM))))
+template <class OP, int BM, int BN, int MS, int BKB, int ST, int WM, int WN, int EPI, typename OutT,
+          bool DEQ>
+__global__ __launch_bounds__(64 * WM * WN)
+__attribute__((amdgpu_waves_per_eu(gemm_waves_per_eu(GemmCfg<OP, BM, BN, MS, BKB, ST, WM, WN>::SMEM,
+                                                     WM * WN))))
 void gemm_mfma_kernel(GemmParams p) {
-  typedef GemmCfg<OP, BM, BN, MS, BKB, ST> G;
+  typedef GemmCfg<OP, BM, BN, MS, BKB, ST, WM, WN> G;
   typedef typename OP::template Mma<MS> MM;
   typedef typename OP::Frag Frag;
   constexpr int TM = G::TM, TN = G::TN, IA = G::IA, IB = G::IB, CH = G::CH;
@@ -236,7 +241,7 @@ void gemm_mfma_kernel(GemmParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   int tm, tn;
   tile_of(blockIdx.x, gridDim.x, p, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
@@ -454,15 +459,20 @@ void gemm_mfma_kernel(GemmParams p) {
 }
 
 // ------------------------------------------------------------ dispatch ----
-// Tile configurations (BM, BN, MS, BKB, ST); the choice rule is in pick_cfg.
-//   0: 256x256, 32x32 MFMA, 64-byte slices, 4-stage ring (1 WG/CU)
+// Tile configurations (BM, BN, MS, BKB, ST, wave grid); the choice rule is
+// in pick_cfg.
+//   0: 256x256, 32x32 MFMA, 128-byte slices, 2-stage ring, 8 waves (2 x 4)
 //   1: 128x128, 32x32, 128-byte slices, 2-stage ring (2 WG/CU)
 //   2: 128x96,  16x16, 128-byte slices, 2-stage ring (2 WG/CU)
 //   3: 64x64,   16x16, 128-byte slices, 2-stage ring (up to 5 WG/CU)
 //   4: 128x128, 32x32, 128-byte slices, 3-stage ring (1 WG/CU)
-constexpr int kNumCfgs = 5;
+//   5: 256x192, 32x32, 128-byte slices, 2-stage ring, 8 waves (4 x 2)
+// The 8-wave tiles put two wavefronts of one workgroup on every SIMD, so
+// one wave's barrier or memory wait is covered by the other's MFMAs.
+constexpr int kNumCfgs = 6;
 
-template <class OP, int BM, int BN, int MS, int BKB, int ST, typename OutT, bool DEQ>
+template <class OP, int BM, int BN, int MS, int BKB, int ST, typename OutT, bool DEQ, int WM = 2,
+          int WN = 2>
 static void launch_epi(GemmParams p, int epi, hipStream_t s) {
   p.tiles_n = (p.N + BN - 1) / BN;
   p.tiles_m = (p.M + BM - 1) / BM;
@@ -473,7 +483,8 @@ static void launch_epi(GemmParams p, int epi, hipStream_t s) {
   const int per_xcd = (grid + 7) / 8;
   while (gm * 2 <= p.tiles_m && gm * gm * 4 <= per_xcd) gm *= 2;
   p.group_m = gm;
-#define ZK_L(E) gemm_mfma_kernel<OP, BM, BN, MS, BKB, ST, E, OutT, DEQ><<<grid, 256, 0, s>>>(p)
+#define ZK_L(E) \
+  gemm_mfma_kernel<OP, BM, BN, MS, BKB, ST, WM, WN, E, OutT, DEQ><<<grid, 64 * WM * WN, 0, s>>>(p)
   switch (epi) {
     case ZK_EPI_NONE: ZK_L(ZK_EPI_NONE); break;
     case ZK_EPI_BIAS: ZK_L(ZK_EPI_BIAS); break;
@@ -485,11 +496,15 @@ static void launch_epi(GemmParams p, int epi, hipStream_t s) {
 #undef ZK_L
 }
 
-// Shape -> configuration, from measurements at M = 4096 (bench.py kernels):
+// Shape -> configuration, from measurements at the BERT shapes (M = 4096)
+// and at square sizes:
+//   M >= 1024 and >= 256 tiles of 256x256 (4096^3 and up): the 8-wave
+//     256x256 tile;
 //   N <= 1024 (out-projection, FFN-down): 64x64 tiles for short K keep every
 //     CU busy; for K >= 2048 the 3-stage 128x128 ring hides more latency;
-//   N >= 2048: 128x128 once that gives >= 640 tiles (FFN-up), else 128x96
-//     (QKV); very large problems take 256x256.
+//   M >= 1024 and >= 160 tiles of 256x192 (FFN-up: 256, QKV: 192): the
+//     8-wave 256x192 tile;
+//   otherwise 128x128 once that gives >= 640 tiles, else 128x96.
 // ZK_GEMM_CFG=<id> forces a configuration (tuning runs).
 static int pick_cfg(int M, int N, int K) {
   static int forced = -2;
@@ -498,20 +513,22 @@ static int pick_cfg(int M, int N, int K) {
     forced = e ? atoi(e) : -1;
   }
   if (forced >= 0 && forced < kNumCfgs) return forced;
-  const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
-  if (t128 >= 2048) return 0;
+  const int64_t tm256 = (M + 255) / 256;
+  if (M >= 1024 && N > 1024 && tm256 * ((N + 255) / 256) >= 256) return 0;
   if (N <= 1024) return K >= 2048 ? 4 : 3;
-  if (t128 >= 640) return 1;
-  return 2;
+  if (M >= 1024 && tm256 * ((N + 191) / 192) >= 160) return 5;
+  const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+  return t128 >= 640 ? 1 : 2;
 }
 
 template <class OP, typename OutT, bool DEQ>
 static void launch_mfma(GemmParams p, int epi, hipStream_t s) {
   switch (pick_cfg(p.M, p.N, p.K)) {
-    case 0: launch_epi<OP, 256, 256, 32, 64, 4, OutT, DEQ>(p, epi, s); break;
+    case 0: launch_epi<OP, 256, 256, 32, 128, 2, OutT, DEQ, 2, 4>(p, epi, s); break;
     case 1: launch_epi<OP, 128, 128, 32, 128, 2, OutT, DEQ>(p, epi, s); break;
     case 2: launch_epi<OP, 128, 96, 16, 128, 2, OutT, DEQ>(p, epi, s); break;
     case 4: launch_epi<OP, 128, 128, 32, 128, 3, OutT, DEQ>(p, epi, s); break;
+    case 5: launch_epi<OP, 256, 192, 32, 128, 2, OutT, DEQ, 4, 2>(p, epi, s); break;
     default: launch_epi<OP, 64, 64, 16, 128, 2, OutT, DEQ>(p, epi, s); break;
   }
 }
