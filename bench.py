@@ -113,16 +113,23 @@ def kernel_cases(torch, dev):
                 "TFLOP/s", "fp16", "mfma", f"M={M} K={K} N={N}"
         return setup
 
-    def gemm_i8(M, K, N, epi):
+    def gemm_i8(M, K, N, epi, requant=False):
+        """requant: int8 output re-quantised in the epilogue (the encoder's
+        FFN-up), else fp16 output."""
         def setup():
             a = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev)
             w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev)
             sw = torch.full((N,), 1e-3, dtype=torch.float32, device=dev)
             b = torch.zeros(N, dtype=f16, device=dev)
-            c = torch.empty((M, N), dtype=f16, device=dev)
+            c = torch.empty((M, N), dtype=torch.int8 if requant else f16, device=dev)
+            keep = (a, w, sw, b, c)
+            if requant:
+                args = (a.data_ptr(), w.data_ptr(), c.data_ptr(), M, N, K, K, K, N, 0.01,
+                        sw.data_ptr(), b.data_ptr(), epi, 0.05, s())
+                return (lambda i: _rc(L, lib.zk_gemm_i8_requant(*args)) and keep), \
+                    2.0 * M * N * K, "TOP/s", "int8", "mfma", f"M={M} K={K} N={N} int8 out"
             args = (a.data_ptr(), w.data_ptr(), c.data_ptr(), M, N, K, K, K, N, 0.01,
                     sw.data_ptr(), b.data_ptr(), None, 0, epi, L.ZK_F16, s())
-            keep = (a, w, sw, b, c)
             return (lambda i: _rc(L, lib.zk_gemm_i8(*args)) and keep), 2.0 * M * N * K, \
                 "TOP/s", "int8", "mfma", f"M={M} K={K} N={N}"
         return setup
@@ -209,7 +216,7 @@ def kernel_cases(torch, dev):
         "gemm_sq8192": gemm(8192, 8192, 8192, L.ZK_EPI_NONE),
         "attn_s128": attn(128),
         "attn_s512": attn(512),
-        "int8_ffn_up": gemm_i8(4096, 768, 3072, L.ZK_EPI_BIAS_GELU_ERF),
+        "int8_ffn_up": gemm_i8(4096, 768, 3072, L.ZK_EPI_BIAS_GELU_ERF, requant=True),
         "int8_ffn_down": gemm_i8(4096, 3072, 768, E),
         "add_layernorm": add_ln(),
         "bias_gelu": bias_gelu(),

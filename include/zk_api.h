@@ -78,6 +78,16 @@ int zk_layernorm(const void *x, const void *residual, const void *gamma,
                  const void *beta, void *y, int64_t rows, int64_t hidden,
                  float eps, int dtype, void *stream);
 
+/* zk_layernorm (fp16) that also writes q = quant(y, q_scale) as int8
+ * [rows, hidden] (quant as in zk_quantize_i8, applied to the fp16 output),
+ * for an int8 GEMM that consumes the normalised rows. Equals zk_layernorm
+ * followed by zk_quantize_i8 on y: fused_add_layernorm
+ * (fused_kernels.cu:145-221) followed by quantize_f32_to_int8_kernel
+ * (cuda_kernels.cu:918-937). */
+int zk_layernorm_q8(const void *x, const void *residual, const void *gamma,
+                    const void *beta, void *y, int8_t *q, int64_t rows,
+                    int64_t hidden, float eps, float q_scale, void *stream);
+
 /* Out-of-place transpose of a [rows, cols] fp16 matrix (leading dim lds)
  * into [cols, rows] (leading dim ldd). Used to present B[K,N] as the
  * K-major operand the MFMA GEMM reads.
@@ -144,6 +154,20 @@ int zk_gemm_i8(const int8_t *A, const int8_t *W, void *C, int64_t M,
                float s_x, const float *s_w, const void *bias,
                const void *residual, int64_t ldr, int epilogue,
                int out_dtype, void *stream);
+
+/* INT8 GEMM whose output is re-quantised for the next int8 GEMM:
+ *   Q[m,n] = quant(fp16(epilogue(acc[m,n] * (s_x * s_w[n]) + bias[n])), s_out)
+ * with quant as in zk_quantize_i8; bias fp16 [N]; epilogue NONE, BIAS,
+ * BIAS_GELU_ERF, BIAS_GELU_TANH or BIAS_RELU. Q is int8 [M, ldq].
+ * Equals zk_gemm_i8 (out_dtype ZK_F16) followed by zk_quantize_i8 on its
+ * output, without the fp16 intermediate: the FFN-up -> quantise step of the
+ * INT8 FFN (fused_int8_linear cuda_kernels.cu:1010-1049 followed by
+ * quantize_f32_to_int8_kernel :918-937; numpy form
+ * benchmarks/int8_bench.py:19-45). */
+int zk_gemm_i8_requant(const int8_t *A, const int8_t *W, int8_t *Q, int64_t M,
+                       int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldq,
+                       float s_x, const float *s_w, const void *bias, int epilogue,
+                       float s_out, void *stream);
 
 #ifdef __cplusplus
 }

@@ -100,3 +100,70 @@ def test_int8_ffn_config4(dev):
     d32 = ops.linear(ops.bias_gelu(ops.linear(x, w["Wi"]), w["bi"], "erf"), w["Wo2"], w["bo2"])
     snr = 10 * np.log10(np.sum(d32**2) / np.sum((d.float().cpu().numpy() - d32) ** 2))
     assert snr > 20, snr
+
+
+@pytest.mark.parametrize("rows,hidden", [(4096, 768), (333, 768), (7, 100), (64, 2048)])
+def test_add_layernorm_q8(dev, rows, hidden):
+    """LN output identical to add_layernorm, int8 output identical to
+    quantising it (on the GPU and in the oracle); hidden=100 takes the
+    generic block-per-row kernel."""
+    from zenith_amd import zenith_cuda as zc
+
+    x = synthetic.round_f16(synthetic.normal((rows, hidden), tag=40))
+    r = synthetic.round_f16(synthetic.normal((rows, hidden), tag=41))
+    g = synthetic.round_f16(1.0 + synthetic.normal((hidden,), tag=42, std=0.1))
+    b = synthetic.round_f16(synthetic.normal((hidden,), tag=43, std=0.1))
+    T = lambda a: torch.from_numpy(a).to(dev, torch.float16)  # noqa: E731
+    s = 4.0 / 127  # |y| up to ~4: saturation and half-way ties both occur
+    y, q = zc.add_layernorm_q8(T(x), T(r), T(g), T(b), 1e-12, s)
+    y2 = zc.add_layernorm(T(x), T(r), T(g), T(b), 1e-12)
+    assert torch.equal(y, y2)
+    np.testing.assert_array_equal(q.cpu().numpy(), zc.quantize_int8(y2, s).cpu().numpy())
+    np.testing.assert_array_equal(q.cpu().numpy(), ops.quantize_int8(y.float().cpu().numpy(), s))
+
+
+@pytest.mark.parametrize("act", [None, "gelu", "relu"])
+@pytest.mark.parametrize("M,K,N", [(4096, 768, 3072), (300, 784, 37)])
+def test_int8_linear_q8(dev, act, M, K, N):
+    """Re-quantising epilogue == int8_linear (fp16 out) then quantize_int8,
+    bit for bit; vs the oracle within one quantisation step (the fp16 value
+    may sit on the other side of a rounding boundary)."""
+    from zenith_amd import zenith_cuda as zc
+
+    x = synthetic.normal((M, K), tag=44)
+    wf = synthetic.normal((N, K), tag=45, std=0.02)
+    b = synthetic.round_f16(synthetic.normal((N,), tag=46, std=0.1))
+    s_x = ops.absmax_scale(np.abs(x).max())
+    qx = ops.quantize_int8(x, s_x)
+    qw, s_w = ops.quantize_weight_per_channel(wf)
+    args = (torch.from_numpy(qx).to(dev), torch.from_numpy(qw).to(dev), float(s_x),
+            torch.from_numpy(s_w).to(dev), torch.from_numpy(b).to(dev, torch.float16))
+    s_out = 0.5 / 127
+    q = zc.int8_linear_q8(*args, activation=act, s_out=s_out).cpu().numpy()
+    two = zc.quantize_int8(zc.int8_linear(*args, activation=act), s_out).cpu().numpy()
+    np.testing.assert_array_equal(q, two)
+    ref = ops.quantize_int8(ops.int8_linear(qx, qw, s_x, s_w, b, act), s_out)
+    diff = np.abs(q.astype(np.int32) - ref.astype(np.int32))
+    assert diff.max() <= 1 and (diff == 0).mean() > 0.95, (diff.max(), (diff == 0).mean())
+
+
+@pytest.mark.parametrize("scale", [4 / 127, 0.5 / 127, 0.01, 3.7e-3, 0.123])
+def test_quantize_near_ties(dev, scale):
+    """Values within a few ulps of (k + 1/2) * scale, where rounding the
+    quotient decides the result: the kernels multiply by 1/scale and fall
+    back to the IEEE division near ties; the answer must equal
+    rint(float32(x / scale)) everywhere (fp32 and fp16 inputs)."""
+    from zenith_amd import zenith_cuda as zc
+
+    rng = np.random.default_rng(int(scale * 1e6))
+    s = np.float32(scale)
+    x = ((rng.integers(-140, 140, 1 << 18) + 0.5) * s).astype(np.float32)
+    for _ in range(4):
+        step = rng.integers(-1, 2, x.size)
+        x = np.where(step == 0, x, np.nextafter(x, np.where(step > 0, np.inf, -np.inf).astype(np.float32)))
+    x = np.concatenate([x.astype(np.float32), rng.normal(0, 60 * scale, 1 << 16).astype(np.float32)])
+    q = zc.quantize_int8(torch.from_numpy(x).to(dev), float(s)).cpu().numpy()
+    np.testing.assert_array_equal(q, ops.quantize_int8(x, s))
+    xh = x.astype(np.float16)
+    qh = zc.quantize_int8(torch.from_numpy(xh).to(dev), float(s)).cpu().numpy()
+    np.testing.assert_array_equal(qh, ops.quantize_int8(xh.astype(np.float32), s))

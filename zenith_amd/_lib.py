@@ -41,6 +41,7 @@ SIGNATURES: dict[str, list] = {
     "zk_relu": [_vp, _vp, _i64, _i32, _vp],
     "zk_gelu": [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp],
     "zk_layernorm": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp],
+    "zk_layernorm_q8": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _f32, _vp],
     "zk_transpose_f16": [_vp, _vp, _i64, _i64, _i64, _i64, _vp],
     "zk_gemm_f16": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
                     _vp, _vp, _i64, _i32, _vp],
@@ -50,6 +51,8 @@ SIGNATURES: dict[str, list] = {
     "zk_quantize_i8": [_vp, _vp, _i64, _f32, _i32, _vp],
     "zk_gemm_i8": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _vp,
                    _vp, _vp, _i64, _i32, _i32, _vp],
+    "zk_gemm_i8_requant": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _vp,
+                           _vp, _i32, _f32, _vp],
 }
 _RESTYPES = {"zk_last_error": ctypes.c_char_p}
 

@@ -31,7 +31,27 @@ int check_launch(const char *what);
 __host__ __device__ inline bool aligned16(const void *p) {
   return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
+__host__ __device__ inline bool aligned8(const void *p) {
+  return (reinterpret_cast<uintptr_t>(p) & 7u) == 0;
+}
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Symmetric int8 quantisation of one value,
+//   q = clamp(round_half_even(RN(x / scale)), -128, 127)
+// (quantize_f32_to_int8_kernel, core/src/cuda_kernels.cu:926-927), with
+// inv = RN(1 / scale) computed once by the caller. t = RN(x * inv) is within
+// 3 * 2^-24 |x / scale| of RN(x / scale) (three roundings of at most 2^-24
+// each), i.e. within 2.4e-5 for |t| < 129, so rint(t) is the exact answer
+// unless t lies within 6e-5 of a half-integer; those values (about one in
+// ten thousand) take the IEEE division (hipcc keeps fp32 '/' correctly
+// rounded). For |t| >= 129 both forms saturate, whichever path is taken.
+__device__ __forceinline__ int8_t quant1(float x, float scale, float inv) {
+  const float t = x * inv;
+  float r = __builtin_rintf(t);
+  if (fabsf(t - r) >= 0.49994f) r = __builtin_rintf(x / scale);
+  r = fminf(fmaxf(r, -128.0f), 127.0f);
+  return (int8_t)(int)r;
+}
 
 // ------------------------------------------------------------ device math --
 __device__ __forceinline__ float gelu_erf(float x) {
@@ -44,29 +64,31 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return 0.5f * x * (1.0f + tanhf(inner));
 }
 
-// Branch-free forms for GEMM epilogues (fp16 outputs).
+// Branch-free forms for GEMM epilogues (fp16 outputs), with the constant
+// factors folded so that each costs as few VALU instructions as possible.
 // erf by Abramowitz & Stegun 7.1.26: for z >= 0,
 //   erf(z) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-z^2),
 //   t = 1 / (1 + p z), |error| <= 1.5e-7.
+// With z = |x| / sqrt(2) and h = (1 - erf(z)) / 2 (the halves folded into
+// the a_k): GELU(x) = x (1 - h) for x >= 0 and x h for x < 0.
 __device__ __forceinline__ float gelu_erf_fast(float x) {
-  const float z = fabsf(x) * 0.70710678118654752f;
-  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * z);
-  float q = 1.061405429f;
-  q = q * t - 1.453152027f;
-  q = q * t + 1.421413741f;
-  q = q * t - 0.284496736f;
-  q = q * t + 0.254829592f;
-  q *= t;
-  // 1 - erf(z), then GELU = 0.5 x (1 + sign(x) erf(|x| / sqrt 2))
-  const float tail = q * __builtin_amdgcn_exp2f(-z * z * 1.4426950408889634f);
-  return x >= 0.f ? x - 0.5f * x * tail : 0.5f * x * tail;
+  const float t = __builtin_amdgcn_rcpf(fmaf(fabsf(x), 0.3275911f * 0.70710678118654752f, 1.0f));
+  float q = 0.5f * 1.061405429f;
+  q = fmaf(q, t, 0.5f * -1.453152027f);
+  q = fmaf(q, t, 0.5f * 1.421413741f);
+  q = fmaf(q, t, 0.5f * -0.284496736f);
+  q = fmaf(q, t, 0.5f * 0.254829592f);
+  // exp(-z^2) = exp2(-x^2 log2(e) / 2)
+  const float h = q * t * __builtin_amdgcn_exp2f(x * x * (-0.5f * 1.4426950408889634f));
+  return x * (x >= 0.f ? 1.0f - h : h);
 }
-// tanh(y) = 1 - 2 / (1 + exp(2y)): exact identity, one exp and one reciprocal.
+// tanh(y) = 1 - 2 / (1 + exp(2y)) (exact identity), so
+// 0.5 x (1 + tanh(y)) = x - x / (1 + exp(2y)), y = sqrt(2/pi) (x + 0.044715 x^3).
 __device__ __forceinline__ float gelu_tanh_fast(float x) {
-  const float y = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-  const float e = __builtin_amdgcn_exp2f(2.0f * 1.4426950408889634f * y);
-  const float th = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
-  return 0.5f * x * (1.0f + th);
+  constexpr float c1 = 2.0f * 1.4426950408889634f * 0.7978845608028654f;
+  constexpr float c3 = c1 * 0.044715f;
+  const float e = __builtin_amdgcn_exp2f(x * fmaf(c3, x * x, c1));
+  return fmaf(-x, __builtin_amdgcn_rcpf(1.0f + e), x);
 }
 
 // Butterfly sum / max across the 64 lanes of a wavefront.

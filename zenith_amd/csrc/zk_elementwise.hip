@@ -123,16 +123,10 @@ static int gelu_impl(const void *x, const void *bias, void *y, int64_t n,
 }
 
 // -------------------------------------------------------------- quantise --
-__device__ __forceinline__ int8_t quant1(float x, float scale) {
-  // IEEE division (hipcc keeps fp32 '/' correctly rounded), then
-  // round-half-to-even and saturate to the int8 range.
-  float r = __builtin_rintf(x / scale);
-  r = fminf(fmaxf(r, -128.0f), 127.0f);
-  return (int8_t)(int)r;
-}
 
 __global__ void quant_f16_vec(const f16 *__restrict__ x, int8_t *__restrict__ q,
                               int64_t nvec, float scale) {
+  const float inv = 1.0f / scale;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nvec;
        i += stride) {
@@ -140,8 +134,8 @@ __global__ void quant_f16_vec(const f16 *__restrict__ x, int8_t *__restrict__ q,
     uint32_t lo = 0, hi = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      lo |= (uint32_t)(uint8_t)quant1((float)v[j], scale) << (8 * j);
-      hi |= (uint32_t)(uint8_t)quant1((float)v[j + 4], scale) << (8 * j);
+      lo |= (uint32_t)(uint8_t)quant1((float)v[j], scale, inv) << (8 * j);
+      hi |= (uint32_t)(uint8_t)quant1((float)v[j + 4], scale, inv) << (8 * j);
     }
     reinterpret_cast<uint2 *>(q)[i] = make_uint2(lo, hi);
   }
@@ -150,10 +144,11 @@ __global__ void quant_f16_vec(const f16 *__restrict__ x, int8_t *__restrict__ q,
 template <typename T>
 __global__ void quant_scalar(const T *__restrict__ x, int8_t *__restrict__ q,
                              int64_t begin, int64_t n, float scale) {
+  const float inv = 1.0f / scale;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = begin + blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
        i < n; i += stride)
-    q[i] = quant1((float)x[i], scale);
+    q[i] = quant1((float)x[i], scale, inv);
 }
 
 // ------------------------------------------------------------- transpose --

@@ -59,6 +59,7 @@ struct GemmParams {
   int tiles_n;
   int tiles_m;
   int group_m;
+  float s_q;  // int8 output: scale of the re-quantisation
 };
 
 #define ZK_LDS(p) ((__attribute__((address_space(3))) void *)(p))
@@ -375,10 +376,15 @@ void gemm_mfma_kernel(GemmParams p) {
 
   // Epilogue: per wave, one MS-row stripe at a time.
   float *ws = (float *)smem + wave * MS * G::EPITCH;
+  // int8 output (re-quantisation): bias and residual are fp16; the value is
+  // rounded to fp16 first, so the result equals quantising the fp16 output.
+  constexpr bool Q8 = std::is_same<OutT, int8_t>::value;
+  typedef typename std::conditional<Q8, f16, OutT>::type BiasT;
   OutT *C = (OutT *)p.C;
-  const OutT *bias = (const OutT *)p.bias;
-  const OutT *res = (const OutT *)p.res;
-  const bool vec_ok = (p.ldc % 8 == 0) && aligned16(p.C) &&
+  const BiasT *bias = (const BiasT *)p.bias;
+  const BiasT *res = (const BiasT *)p.res;
+  const float inv_q = Q8 ? 1.0f / p.s_q : 1.0f;
+  const bool vec_ok = (p.ldc % 8 == 0) && (Q8 ? aligned8(p.C) : aligned16(p.C)) &&
                       (EPI != ZK_EPI_BIAS_RESIDUAL || ((p.ldr % 8 == 0) && aligned16(p.res)));
   float bj[TN], sj[TN];
 #pragma unroll
@@ -423,8 +429,8 @@ void gemm_mfma_kernel(GemmParams p) {
         } else {
           float o[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
           if constexpr (EPI == ZK_EPI_BIAS_RESIDUAL) {
-            const OutT *rp = res + (int64_t)row * p.ldr + col;
-            if constexpr (std::is_same<OutT, f16>::value) {
+            const BiasT *rp = res + (int64_t)row * p.ldr + col;
+            if constexpr (std::is_same<BiasT, f16>::value) {
               const f16x8 rv = *(const f16x8 *)rp;
 #pragma unroll
               for (int e = 0; e < 8; ++e) o[e] += (float)rv[e];
@@ -438,6 +444,14 @@ void gemm_mfma_kernel(GemmParams p) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) h[e] = (f16)o[e];
             *(f16x8 *)dst = h;
+          } else if constexpr (Q8) {
+            uint32_t qlo = 0, qhi = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              qlo |= (uint32_t)(uint8_t)quant1((float)(f16)o[e], p.s_q, inv_q) << (8 * e);
+              qhi |= (uint32_t)(uint8_t)quant1((float)(f16)o[e + 4], p.s_q, inv_q) << (8 * e);
+            }
+            *(uint2 *)dst = make_uint2(qlo, qhi);
           } else {
             *(f32x4 *)dst = f32x4{o[0], o[1], o[2], o[3]};
             *(f32x4 *)(dst + 4) = f32x4{o[4], o[5], o[6], o[7]};
@@ -450,7 +464,8 @@ void gemm_mfma_kernel(GemmParams p) {
           } else {
             float o = src[e];
             if (EPI == ZK_EPI_BIAS_RESIDUAL) o += to_f(res[(int64_t)row * p.ldr + col + e]);
-            dst[e] = (OutT)o;
+            if constexpr (Q8) dst[e] = quant1((float)(f16)o, p.s_q, inv_q);
+            else dst[e] = (OutT)o;
           }
         }
       }
@@ -490,7 +505,9 @@ static void launch_epi(GemmParams p, int epi, hipStream_t s) {
     case ZK_EPI_BIAS: ZK_L(ZK_EPI_BIAS); break;
     case ZK_EPI_BIAS_GELU_ERF: ZK_L(ZK_EPI_BIAS_GELU_ERF); break;
     case ZK_EPI_BIAS_GELU_TANH: ZK_L(ZK_EPI_BIAS_GELU_TANH); break;
-    case ZK_EPI_BIAS_RESIDUAL: ZK_L(ZK_EPI_BIAS_RESIDUAL); break;
+    case ZK_EPI_BIAS_RESIDUAL:
+      if constexpr (!std::is_same<OutT, int8_t>::value) ZK_L(ZK_EPI_BIAS_RESIDUAL);
+      break;
     case ZK_EPI_BIAS_RELU: ZK_L(ZK_EPI_BIAS_RELU); break;
   }
 #undef ZK_L
@@ -635,25 +652,33 @@ extern "C" int zk_gemm_f16(const void *A, const void *B, void *C, int64_t M,
   return check_launch("zk_gemm_f16");
 }
 
+// Shape / operand checks shared by the int8 entry points.
+static int check_i8(const char *who, const int8_t *A, const int8_t *W, const void *C, int64_t M,
+                    int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc, int epilogue) {
+  int st = check_dims(who, M, N, K);
+  if (st) return st;
+  if (M == 0 || N == 0) return ZK_OK;
+  if (!A || !W || !C) return fail(ZK_ERR_INVALID, "%s: null pointer", who);
+  if (epilogue < ZK_EPI_NONE || epilogue > ZK_EPI_BIAS_RELU)
+    return fail(ZK_ERR_INVALID, "%s: bad epilogue %d", who, epilogue);
+  if (lda < K || ldw < K || ldc < N)
+    return fail(ZK_ERR_INVALID, "%s: leading dimension too small", who);
+  if (K % 16 || lda % 16 || ldw % 16 || !aligned16(A) || !aligned16(W))
+    return fail(ZK_ERR_UNSUPPORTED,
+                "%s: K, lda, ldw must be multiples of 16 and A, W 16-byte aligned", who);
+  if (K == 0) return fail(ZK_ERR_UNSUPPORTED, "%s: K == 0", who);
+  if (K > 131072)
+    return fail(ZK_ERR_UNSUPPORTED, "%s: K > 131072 could overflow int32 accumulators", who);
+  return ZK_OK;
+}
+
 extern "C" int zk_gemm_i8(const int8_t *A, const int8_t *W, void *C, int64_t M,
                           int64_t N, int64_t K, int64_t lda, int64_t ldw,
                           int64_t ldc, float s_x, const float *s_w,
                           const void *bias, const void *residual, int64_t ldr,
                           int epilogue, int out_dtype, void *stream) {
-  int st = check_dims("zk_gemm_i8", M, N, K);
-  if (st) return st;
-  if (M == 0 || N == 0) return ZK_OK;
-  if (!A || !W || !C) return fail(ZK_ERR_INVALID, "zk_gemm_i8: null pointer");
-  if (epilogue < ZK_EPI_NONE || epilogue > ZK_EPI_BIAS_RELU)
-    return fail(ZK_ERR_INVALID, "zk_gemm_i8: bad epilogue %d", epilogue);
-  if (lda < K || ldw < K || ldc < N)
-    return fail(ZK_ERR_INVALID, "zk_gemm_i8: leading dimension too small");
-  if (K % 16 || lda % 16 || ldw % 16 || !aligned16(A) || !aligned16(W))
-    return fail(ZK_ERR_UNSUPPORTED,
-                "zk_gemm_i8: K, lda, ldw must be multiples of 16 and A, W 16-byte aligned");
-  if (K == 0) return fail(ZK_ERR_UNSUPPORTED, "zk_gemm_i8: K == 0");
-  if (K > 131072)
-    return fail(ZK_ERR_UNSUPPORTED, "zk_gemm_i8: K > 131072 could overflow int32 accumulators");
+  int st = check_i8("zk_gemm_i8", A, W, C, M, N, K, lda, ldw, ldc, epilogue);
+  if (st || M == 0 || N == 0) return st;
   hipStream_t s = as_stream(stream);
   GemmParams p{A, W, C, (int)M, (int)N, (int)K, lda, ldw, ldc, bias, residual, ldr, s_x, s_w, 0};
   if (out_dtype == ZK_I32) {
@@ -672,6 +697,26 @@ extern "C" int zk_gemm_i8(const int8_t *A, const int8_t *W, void *C, int64_t M,
   else if (out_dtype == ZK_F32) launch_mfma<I8Op, float, true>(p, epilogue, s);
   else return fail(ZK_ERR_UNSUPPORTED, "zk_gemm_i8: out_dtype %d not supported", out_dtype);
   return check_launch("zk_gemm_i8");
+}
+
+extern "C" int zk_gemm_i8_requant(const int8_t *A, const int8_t *W, int8_t *Q, int64_t M,
+                                  int64_t N, int64_t K, int64_t lda, int64_t ldw,
+                                  int64_t ldq, float s_x, const float *s_w,
+                                  const void *bias, int epilogue, float s_out,
+                                  void *stream) {
+  int st = check_i8("zk_gemm_i8_requant", A, W, Q, M, N, K, lda, ldw, ldq, epilogue);
+  if (st || M == 0 || N == 0) return st;
+  if (epilogue == ZK_EPI_BIAS_RESIDUAL)
+    return fail(ZK_ERR_INVALID, "zk_gemm_i8_requant: no residual epilogue for int8 output");
+  if (!s_w) return fail(ZK_ERR_INVALID, "zk_gemm_i8_requant: s_w is required");
+  if (!(s_x > 0.f) || !(s_out > 0.f))
+    return fail(ZK_ERR_INVALID, "zk_gemm_i8_requant: s_x and s_out must be > 0");
+  if (epilogue != ZK_EPI_NONE && !bias)
+    return fail(ZK_ERR_INVALID, "zk_gemm_i8_requant: epilogue needs a bias");
+  GemmParams p{A, W, Q, (int)M, (int)N, (int)K, lda, ldw, ldq, bias, nullptr, 0, s_x, s_w, 0};
+  p.s_q = s_out;
+  launch_mfma<I8Op, int8_t, true>(p, epilogue, as_stream(stream));
+  return check_launch("zk_gemm_i8_requant");
 }
 
 extern "C" int zk_gemm_f32(const float *A, const float *B, float *C, int64_t M,

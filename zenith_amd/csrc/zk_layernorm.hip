@@ -19,11 +19,13 @@ constexpr int kLnWaves = 4;  // wavefronts per 256-thread block
 
 // LPR lanes per row (64 / LPR rows per wavefront): a 768-wide fp16 row is 96
 // 16-byte vectors, so two rows per wavefront give every lane exactly three.
-template <typename T, int MAXV, bool RES, int LPR>
+// Q8: also write q = quant(y) as int8 (the fp16 output value quantised with
+// scale qs), for an int8 GEMM that consumes the normalised rows.
+template <typename T, int MAXV, bool RES, int LPR, bool Q8>
 __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
     const T *__restrict__ x, const T *__restrict__ res,
     const T *__restrict__ gamma, const T *__restrict__ beta, T *__restrict__ y,
-    int64_t rows, int hidden, float eps) {
+    int8_t *__restrict__ q, float qs, int64_t rows, int hidden, float eps) {
   typedef typename LnVec<T>::type V;
   constexpr int W = LnVec<T>::n;
   constexpr int RPW = kWave / LPR;  // rows per wavefront
@@ -92,16 +94,27 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
       for (int j = 0; j < W; ++j)
         o[j] = (T)((v[k][j] - mean) * rstd * (float)g[j] + (float)b[j]);
       yr[idx] = o;
+      if constexpr (Q8) {
+        static_assert(W == 8, "int8 output is written 8 bytes per vector");
+        const float inv = 1.0f / qs;
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          lo |= (uint32_t)(uint8_t)quant1((float)o[j], qs, inv) << (8 * j);
+          hi |= (uint32_t)(uint8_t)quant1((float)o[j + 4], qs, inv) << (8 * j);
+        }
+        reinterpret_cast<uint2 *>(q + row * hidden)[idx] = make_uint2(lo, hi);
+      }
     }
   }
 }
 
 // Generic fallback: one 256-thread block per row, three passes over the row.
-template <typename T, bool RES>
+template <typename T, bool RES, bool Q8>
 __global__ __launch_bounds__(256) void ln_block_kernel(
     const T *__restrict__ x, const T *__restrict__ res,
     const T *__restrict__ gamma, const T *__restrict__ beta, T *__restrict__ y,
-    int64_t hidden, float eps) {
+    int8_t *__restrict__ q, float qs, int64_t hidden, float eps) {
   __shared__ float part[256 / kWave];
   const int64_t row = blockIdx.x;
   const T *xr = x + row * hidden;
@@ -124,58 +137,65 @@ __global__ __launch_bounds__(256) void ln_block_kernel(
   for (int64_t i = tid; i < hidden; i += 256)
     s += (float)xr[i] + (RES ? (float)rr[i] : 0.f);
   const float mean = block_sum(s) / (float)hidden;
-  float q = 0.f;
+  float sq = 0.f;
   for (int64_t i = tid; i < hidden; i += 256) {
     const float d = (float)xr[i] + (RES ? (float)rr[i] : 0.f) - mean;
-    q += d * d;
+    sq += d * d;
   }
-  const float rstd = 1.0f / sqrtf(block_sum(q) / (float)hidden + eps);
+  const float rstd = 1.0f / sqrtf(block_sum(sq) / (float)hidden + eps);
   for (int64_t i = tid; i < hidden; i += 256) {
     const float f = (float)xr[i] + (RES ? (float)rr[i] : 0.f);
-    y[row * hidden + i] = (T)((f - mean) * rstd * (float)gamma[i] + (float)beta[i]);
+    const T o = (T)((f - mean) * rstd * (float)gamma[i] + (float)beta[i]);
+    y[row * hidden + i] = o;
+    if (Q8) q[row * hidden + i] = quant1((float)o, qs, 1.0f / qs);
   }
 }
 
-template <typename T, int MAXV, int LPR>
-static void ln_wave_launch(const T *x, const T *r, const T *g, const T *b, T *y,
-                           int64_t rows, int hidden, float eps, hipStream_t s) {
+template <typename T, int MAXV, int LPR, bool Q8>
+static void ln_wave_launch(const T *x, const T *r, const T *g, const T *b, T *y, int8_t *q,
+                           float qs, int64_t rows, int hidden, float eps, hipStream_t s) {
   constexpr int rows_per_block = kLnWaves * (kWave / LPR);
   const unsigned grid = (unsigned)((rows + rows_per_block - 1) / rows_per_block);
   if (r)
-    ln_wave_kernel<T, MAXV, true, LPR><<<grid, kLnWaves * kWave, 0, s>>>(x, r, g, b, y, rows, hidden, eps);
+    ln_wave_kernel<T, MAXV, true, LPR, Q8><<<grid, kLnWaves * kWave, 0, s>>>(
+        x, r, g, b, y, q, qs, rows, hidden, eps);
   else
-    ln_wave_kernel<T, MAXV, false, LPR><<<grid, kLnWaves * kWave, 0, s>>>(x, r, g, b, y, rows, hidden, eps);
+    ln_wave_kernel<T, MAXV, false, LPR, Q8><<<grid, kLnWaves * kWave, 0, s>>>(
+        x, r, g, b, y, q, qs, rows, hidden, eps);
 }
 
-template <typename T>
+template <typename T, bool Q8>
 static int ln_impl(const void *xv, const void *rv, const void *gv,
-                   const void *bv, void *yv, int64_t rows, int64_t hidden,
-                   float eps, hipStream_t s) {
+                   const void *bv, void *yv, int8_t *q, float qs, int64_t rows,
+                   int64_t hidden, float eps, hipStream_t s) {
   const T *x = (const T *)xv, *r = (const T *)rv, *g = (const T *)gv,
           *b = (const T *)bv;
   T *y = (T *)yv;
   constexpr int W = LnVec<T>::n;
   const bool vec_ok = hidden % W == 0 && aligned16(x) && aligned16(y) &&
-                      aligned16(g) && aligned16(b) && (!r || aligned16(r));
+                      aligned16(g) && aligned16(b) && (!r || aligned16(r)) &&
+                      (!Q8 || aligned8(q));
   const int64_t nvec = hidden / W;
   if (vec_ok && nvec <= 16 * kWave && (rows + kLnWaves - 1) / kLnWaves <= 0x7fffffff) {
     const int h = (int)hidden;
     // 32 lanes per row while a row fits in 4 vectors per lane (H <= 1024 in
     // fp16), else a whole wavefront per row.
-    if (nvec <= 32) ln_wave_launch<T, 1, 32>(x, r, g, b, y, rows, h, eps, s);
-    else if (nvec <= 64) ln_wave_launch<T, 2, 32>(x, r, g, b, y, rows, h, eps, s);
-    else if (nvec <= 96) ln_wave_launch<T, 3, 32>(x, r, g, b, y, rows, h, eps, s);
-    else if (nvec <= 128) ln_wave_launch<T, 4, 32>(x, r, g, b, y, rows, h, eps, s);
-    else if (nvec <= 256) ln_wave_launch<T, 4, 64>(x, r, g, b, y, rows, h, eps, s);
-    else if (nvec <= 512) ln_wave_launch<T, 8, 64>(x, r, g, b, y, rows, h, eps, s);
-    else ln_wave_launch<T, 16, 64>(x, r, g, b, y, rows, h, eps, s);
+#define ZK_LN(MV, LPR) ln_wave_launch<T, MV, LPR, Q8>(x, r, g, b, y, q, qs, rows, h, eps, s)
+    if (nvec <= 32) ZK_LN(1, 32);
+    else if (nvec <= 64) ZK_LN(2, 32);
+    else if (nvec <= 96) ZK_LN(3, 32);
+    else if (nvec <= 128) ZK_LN(4, 32);
+    else if (nvec <= 256) ZK_LN(4, 64);
+    else if (nvec <= 512) ZK_LN(8, 64);
+    else ZK_LN(16, 64);
+#undef ZK_LN
   } else {
     if (rows > 0x7fffffff)
       return fail(ZK_ERR_UNSUPPORTED, "zk_layernorm: too many rows for the generic path");
     if (r)
-      ln_block_kernel<T, true><<<(unsigned)rows, 256, 0, s>>>(x, r, g, b, y, hidden, eps);
+      ln_block_kernel<T, true, Q8><<<(unsigned)rows, 256, 0, s>>>(x, r, g, b, y, q, qs, hidden, eps);
     else
-      ln_block_kernel<T, false><<<(unsigned)rows, 256, 0, s>>>(x, r, g, b, y, hidden, eps);
+      ln_block_kernel<T, false, Q8><<<(unsigned)rows, 256, 0, s>>>(x, r, g, b, y, q, qs, hidden, eps);
   }
   return check_launch("zk_layernorm");
 }
@@ -184,19 +204,37 @@ static int ln_impl(const void *xv, const void *rv, const void *gv,
 
 using namespace zk;
 
+static int ln_check(const char *who, const void *x, const void *gamma, const void *beta,
+                    const void *y, int64_t rows, int64_t hidden, float eps) {
+  if (rows < 0 || hidden < 0) return fail(ZK_ERR_INVALID, "%s: negative size", who);
+  if (rows == 0) return ZK_OK;
+  if (hidden == 0) return fail(ZK_ERR_INVALID, "%s: hidden must be > 0", who);
+  if (!x || !gamma || !beta || !y) return fail(ZK_ERR_INVALID, "%s: null pointer", who);
+  if (!(eps >= 0.0f)) return fail(ZK_ERR_INVALID, "%s: eps must be >= 0", who);
+  return ZK_OK;
+}
+
 extern "C" int zk_layernorm(const void *x, const void *residual,
                             const void *gamma, const void *beta, void *y,
                             int64_t rows, int64_t hidden, float eps, int dtype,
                             void *stream) {
-  if (rows < 0 || hidden < 0)
-    return fail(ZK_ERR_INVALID, "zk_layernorm: negative size");
-  if (rows == 0) return ZK_OK;
-  if (hidden == 0) return fail(ZK_ERR_INVALID, "zk_layernorm: hidden must be > 0");
-  if (!x || !gamma || !beta || !y)
-    return fail(ZK_ERR_INVALID, "zk_layernorm: null pointer");
-  if (!(eps >= 0.0f)) return fail(ZK_ERR_INVALID, "zk_layernorm: eps must be >= 0");
+  int st = ln_check("zk_layernorm", x, gamma, beta, y, rows, hidden, eps);
+  if (st || rows == 0) return st;
   hipStream_t s = as_stream(stream);
-  if (dtype == ZK_F32) return ln_impl<float>(x, residual, gamma, beta, y, rows, hidden, eps, s);
-  if (dtype == ZK_F16) return ln_impl<f16>(x, residual, gamma, beta, y, rows, hidden, eps, s);
+  if (dtype == ZK_F32)
+    return ln_impl<float, false>(x, residual, gamma, beta, y, nullptr, 1.f, rows, hidden, eps, s);
+  if (dtype == ZK_F16)
+    return ln_impl<f16, false>(x, residual, gamma, beta, y, nullptr, 1.f, rows, hidden, eps, s);
   return fail(ZK_ERR_UNSUPPORTED, "zk_layernorm: dtype %d not supported", dtype);
+}
+
+extern "C" int zk_layernorm_q8(const void *x, const void *residual, const void *gamma,
+                               const void *beta, void *y, int8_t *q, int64_t rows,
+                               int64_t hidden, float eps, float q_scale, void *stream) {
+  int st = ln_check("zk_layernorm_q8", x, gamma, beta, y, rows, hidden, eps);
+  if (st || rows == 0) return st;
+  if (!q) return fail(ZK_ERR_INVALID, "zk_layernorm_q8: null pointer");
+  if (!(q_scale > 0.f)) return fail(ZK_ERR_INVALID, "zk_layernorm_q8: q_scale must be > 0");
+  return ln_impl<f16, true>(x, residual, gamma, beta, y, q, q_scale, rows, hidden, eps,
+                            as_stream(stream));
 }

@@ -12,8 +12,12 @@ One post-LN layer is seven launches, in the reference encoder's order
   6. FFN-down GEMM + bias       u . Wo2^T                     -> t[M,H]
   7. Add+LayerNorm              LN(t + h1)                    -> out[M,H]
 
-The INT8-FFN variant replaces 5 and 6 by quantise -> int8 GEMM (dequant +
-bias + GELU epilogue) -> quantise -> int8 GEMM (dequant + bias epilogue).
+The INT8-FFN variant keeps seven launches: step 4 also writes the int8
+quantisation of h1, step 5 is an int8 GEMM whose epilogue dequantises, adds
+the bias, applies GELU and re-quantises (int8 out), and step 6 is an int8
+GEMM with a dequant + bias epilogue. The int8 values equal those of the
+unfused sequence (quantise the fp16 tensor), since both quantise the same
+fp16-rounded value.
 
 All activations live in buffers allocated once per (batch, seq); the whole
 forward can be captured into a HIP graph (torch.cuda.CUDAGraph) and replayed,
@@ -155,19 +159,22 @@ class BertEncoder:
                B, nh, S, S, D, strides, None if lens is None else lens.data_ptr(),
                float(1.0 / np.sqrt(D)), L.ZK_F16, stream)
         self._gemm(ctx, w["Wo"], w["bo"], t, L.ZK_EPI_BIAS, stream=stream)
-        L.call("zk_layernorm", t.data_ptr(), x.data_ptr(), w["ln1_g"].data_ptr(),
-               w["ln1_b"].data_ptr(), h1.data_ptr(), M, H, self.eps, L.ZK_F16, stream)
         if self.int8 is None:
+            L.call("zk_layernorm", t.data_ptr(), x.data_ptr(), w["ln1_g"].data_ptr(),
+                   w["ln1_b"].data_ptr(), h1.data_ptr(), M, H, self.eps, L.ZK_F16, stream)
             self._gemm(h1, w["Wi"], w["bi"], u, self.gelu_epi, stream=stream)
             self._gemm(u, w["Wo2"], w["bo2"], t, L.ZK_EPI_BIAS, stream=stream)
         else:
+            # Add+LN1 also writes the int8 FFN input; FFN-up re-quantises its
+            # GELU output in the epilogue (no fp16 intermediate).
             q = self.int8[i]
             qh, qu = bf["q_h"], bf["q_u"]
-            L.call("zk_quantize_i8", h1.data_ptr(), qh.data_ptr(), M * H, q["s_x"], L.ZK_F16, stream)
-            L.call("zk_gemm_i8", qh.data_ptr(), q["Wi_q"].data_ptr(), u.data_ptr(), M, self.ffn, H,
-                   H, H, self.ffn, q["s_x"], q["s_wi"].data_ptr(), w["bi"].data_ptr(), None, 0,
-                   self.gelu_epi, L.ZK_F16, stream)
-            L.call("zk_quantize_i8", u.data_ptr(), qu.data_ptr(), M * self.ffn, q["s_h"], L.ZK_F16, stream)
+            L.call("zk_layernorm_q8", t.data_ptr(), x.data_ptr(), w["ln1_g"].data_ptr(),
+                   w["ln1_b"].data_ptr(), h1.data_ptr(), qh.data_ptr(), M, H, self.eps,
+                   q["s_x"], stream)
+            L.call("zk_gemm_i8_requant", qh.data_ptr(), q["Wi_q"].data_ptr(), qu.data_ptr(), M,
+                   self.ffn, H, H, H, self.ffn, q["s_x"], q["s_wi"].data_ptr(),
+                   w["bi"].data_ptr(), self.gelu_epi, q["s_h"], stream)
             L.call("zk_gemm_i8", qu.data_ptr(), q["Wo2_q"].data_ptr(), t.data_ptr(), M, H, self.ffn,
                    self.ffn, self.ffn, H, q["s_h"], q["s_wo2"].data_ptr(), w["bo2"].data_ptr(),
                    None, 0, L.ZK_EPI_BIAS, L.ZK_F16, stream)

@@ -131,6 +131,31 @@ def add_layernorm(input: torch.Tensor, residual: torch.Tensor | None,
     return out
 
 
+def add_layernorm_q8(input: torch.Tensor, residual: torch.Tensor | None,
+                     gamma: torch.Tensor, beta: torch.Tensor, eps: float,
+                     q_scale: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp16 LayerNorm(input + residual) and its int8 quantisation with scale
+    q_scale in one pass: returns (y, quantize_int8(y, q_scale)) — the
+    fused_add_layernorm -> quantize_f32_to_int8_kernel sequence
+    (core/src/fused_kernels.cu:145-221, core/src/cuda_kernels.cu:918-937)."""
+    _need_cuda(input, residual, gamma, beta)
+    if input.dim() != 2 or input.dtype != torch.float16:
+        raise RuntimeError("add_layernorm_q8: input must be 2D float16 [batch, hidden]")
+    rows, hidden = input.shape
+    for t, name in ((gamma, "gamma"), (beta, "beta")):
+        if t.dtype != input.dtype or t.numel() != hidden:
+            raise RuntimeError(f"{name} must be [hidden] with the input dtype")
+    if residual is not None and (residual.shape != input.shape or residual.dtype != input.dtype):
+        raise RuntimeError("residual must match input shape and dtype")
+    x = input.contiguous()
+    r = residual.contiguous() if residual is not None else None
+    out = torch.empty_like(x)
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    L.call("zk_layernorm_q8", _p(x), _p(r), _p(gamma.contiguous()), _p(beta.contiguous()),
+           _p(out), _p(q), rows, hidden, float(eps), float(q_scale), _stream(x))
+    return out, q
+
+
 # ------------------------------------------------------------------ GEMMs ---
 def _pad_k(t: torch.Tensor, mult: int) -> torch.Tensor:
     k = t.shape[-1]
@@ -417,8 +442,41 @@ def int8_linear(a_q: torch.Tensor, w_q: torch.Tensor, s_x: float, s_w: torch.Ten
     return out
 
 
+def int8_linear_q8(a_q: torch.Tensor, w_q: torch.Tensor, s_x: float, s_w: torch.Tensor,
+                   bias: torch.Tensor | None, activation: str | None,
+                   s_out: float) -> torch.Tensor:
+    """quantize_int8(int8_linear(a_q, w_q, s_x, s_w, bias, activation), s_out)
+    in one kernel: the dequantised, biased, activated fp16 value is
+    re-quantised in the GEMM epilogue (int8 out, no fp16 intermediate)."""
+    _need_cuda(a_q, w_q, s_w, bias)
+    if a_q.dtype != torch.int8 or w_q.dtype != torch.int8:
+        raise RuntimeError("int8_linear_q8 expects int8 operands")
+    if a_q.dim() != 2 or w_q.dim() != 2 or a_q.shape[1] != w_q.shape[1]:
+        raise RuntimeError("int8_linear_q8: expected a[M,K] and w[N,K]")
+    if activation not in _ACT_EPI:
+        raise RuntimeError(f"int8_linear_q8: unsupported activation {activation!r}")
+    a_q, w_q = _pad_k(a_q, 16), _pad_k(w_q, 16)
+    M, K = a_q.shape
+    N = w_q.shape[0]
+    s_w = s_w.to(torch.float32).contiguous()
+    if s_w.numel() != N:
+        raise RuntimeError("int8_linear_q8: s_w must be [out_features]")
+    b = bias
+    if b is None and activation is not None:
+        b = torch.zeros(N, dtype=torch.float16, device=a_q.device)
+    if b is not None:
+        b = b.to(torch.float16).contiguous()
+    epi = L.ZK_EPI_NONE if b is None else _ACT_EPI[activation]
+    out = torch.empty((M, N), dtype=torch.int8, device=a_q.device)
+    if M and N:
+        L.call("zk_gemm_i8_requant", _p(a_q), _p(w_q), _p(out), M, N, K, a_q.stride(0),
+               w_q.stride(0), out.stride(0), float(s_x), _p(s_w), _p(b), epi, float(s_out),
+               _stream(a_q))
+    return out
+
+
 __all__ = [
     "relu", "gelu", "layernorm", "matmul", "flash_attention", "wmma_matmul",
-    "add_layernorm", "bias_gelu", "linear", "transpose_f16",
-    "quantize_int8", "int8_matmul", "int8_linear",
+    "add_layernorm", "add_layernorm_q8", "bias_gelu", "linear", "transpose_f16",
+    "quantize_int8", "int8_matmul", "int8_linear", "int8_linear_q8",
 ]
