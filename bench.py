@@ -9,7 +9,8 @@ replayed from a HIP graph, inputs resident in HBM. Prints ONE JSON line with:
   value / ms_per_step  fp16 encoder (the INT8-FFN variant in `int8_ffn`)
   roofline             the dominant kernel (FFN-up GEMM, 4096x768 -> 3072,
                        bias + erf-GELU epilogue, 2*M*N*K = 19.33 GFLOP per
-                       launch) timed with HIP events on its launch stream;
+                       launch) timed with HIP events around a HIP-graph
+                       replay of back-to-back launches on that stream;
                        `traffic` from the rocprofv3 FETCH_SIZE / WRITE_SIZE
                        summary in profiles/gemm_ffn_up_pmc.md when present
   kernels              per-kernel times and roofline fractions for the
@@ -64,18 +65,30 @@ def _args():
 
 # ------------------------------------------------------------------ timing --
 def time_launches(torch, launch, n_iter=50, n_warm=5):
-    """Average duration (s) of launch() over n_iter back-to-back launches,
-    bracketed by HIP events on the current stream (the stream every
-    zenith_amd launch goes to)."""
+    """Average duration (s) of launch() over n_iter back-to-back launches.
+
+    The launches are captured once into a HIP graph and the graph replay is
+    bracketed by HIP events on the capture stream (the stream every
+    zenith_amd launch of the replay goes to). Eager launches from Python
+    cost ~6 us of host time each, which would hide the GPU time of every
+    kernel shorter than that; the replay issues them back to back."""
     for _ in range(n_warm):
         launch(0)
-    stream = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(n_iter):
+                launch(i)
+    torch.cuda.synchronize()
+    graph.replay()  # warm replay
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record(stream)
-    for i in range(n_iter):
-        launch(i)
+    with torch.cuda.stream(stream):
+        graph.replay()
     e1.record(stream)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / 1e3 / n_iter
@@ -105,11 +118,10 @@ def kernel_cases(torch, dev):
             w = torch.from_numpy(synthetic.uniform((N, K), tag=2)).to(dev, f16) * 0.05
             b = torch.zeros(N, dtype=f16, device=dev)
             c = torch.empty((M, N), dtype=f16, device=dev)
-            st = s()
             args = (a.data_ptr(), w.data_ptr(), c.data_ptr(), M, N, K, K, K, N, 1, L.ZK_F16,
-                    b.data_ptr(), None, 0, epi, st)
+                    b.data_ptr(), None, 0, epi)
             keep = (a, w, b, c)
-            return (lambda i: _rc(L, lib.zk_gemm_f16(*args)) and keep), 2.0 * M * N * K, \
+            return (lambda i: _rc(L, lib.zk_gemm_f16(*args, s())) and keep), 2.0 * M * N * K, \
                 "TFLOP/s", "fp16", "mfma", f"M={M} K={K} N={N}"
         return setup
 
@@ -125,12 +137,12 @@ def kernel_cases(torch, dev):
             keep = (a, w, sw, b, c)
             if requant:
                 args = (a.data_ptr(), w.data_ptr(), c.data_ptr(), M, N, K, K, K, N, 0.01,
-                        sw.data_ptr(), b.data_ptr(), epi, 0.05, s())
-                return (lambda i: _rc(L, lib.zk_gemm_i8_requant(*args)) and keep), \
+                        sw.data_ptr(), b.data_ptr(), epi, 0.05)
+                return (lambda i: _rc(L, lib.zk_gemm_i8_requant(*args, s())) and keep), \
                     2.0 * M * N * K, "TOP/s", "int8", "mfma", f"M={M} K={K} N={N} int8 out"
             args = (a.data_ptr(), w.data_ptr(), c.data_ptr(), M, N, K, K, K, N, 0.01,
-                    sw.data_ptr(), b.data_ptr(), None, 0, epi, L.ZK_F16, s())
-            return (lambda i: _rc(L, lib.zk_gemm_i8(*args)) and keep), 2.0 * M * N * K, \
+                    sw.data_ptr(), b.data_ptr(), None, 0, epi, L.ZK_F16)
+            return (lambda i: _rc(L, lib.zk_gemm_i8(*args, s())) and keep), 2.0 * M * N * K, \
                 "TOP/s", "int8", "mfma", f"M={M} K={K} N={N}"
         return setup
 
@@ -144,9 +156,9 @@ def kernel_cases(torch, dev):
             strides = L.strides_arg([*q.stride()[:3], *k.stride()[:3], *v.stride()[:3],
                                      *o.stride()[:3]])
             args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), B, H, S, S, D,
-                    strides, lens.data_ptr(), 1.0 / math.sqrt(D), L.ZK_F16, s())
+                    strides, lens.data_ptr(), 1.0 / math.sqrt(D), L.ZK_F16)
             keep = (q, k, v, o, lens, strides)
-            return (lambda i: _rc(L, lib.zk_flash_attn_fwd(*args)) and keep), \
+            return (lambda i: _rc(L, lib.zk_flash_attn_fwd(*args, s())) and keep), \
                 4.0 * B * H * S * S * D, "TFLOP/s", "fp16", "mfma", \
                 f"B={B} H={H} S={S} D={D} lens~U{{S/2..S}} (dense FLOPs)"
         return setup
@@ -161,13 +173,12 @@ def kernel_cases(torch, dev):
             ys = [torch.empty(M, H, device=dev, dtype=f16) for _ in range(n)]
             g = torch.ones(H, device=dev, dtype=f16)
             b = torch.zeros(H, device=dev, dtype=f16)
-            st = s()
             keep = (xs, rs, ys, g, b)
 
             def launch(i):
                 j = i % n
                 _rc(L, lib.zk_layernorm(xs[j].data_ptr(), rs[j].data_ptr(), g.data_ptr(),
-                                        b.data_ptr(), ys[j].data_ptr(), M, H, 1e-12, L.ZK_F16, st))
+                                        b.data_ptr(), ys[j].data_ptr(), M, H, 1e-12, L.ZK_F16, s()))
                 return keep
             return launch, float(per), "GB/s", "hbm", "hbm", \
                 f"[{M},{H}] fp16, {n} rotating buffer sets"
@@ -181,13 +192,12 @@ def kernel_cases(torch, dev):
             xs = [torch.randn(M, N, device=dev, dtype=f16) for _ in range(n)]
             ys = [torch.empty(M, N, device=dev, dtype=f16) for _ in range(n)]
             b = torch.randn(N, device=dev, dtype=f16)
-            st = s()
             keep = (xs, ys, b)
 
             def launch(i):
                 j = i % n
                 _rc(L, lib.zk_gelu(xs[j].data_ptr(), b.data_ptr(), ys[j].data_ptr(), M, N,
-                                   L.ZK_GELU_ERF, L.ZK_F16, st))
+                                   L.ZK_GELU_ERF, L.ZK_F16, s()))
                 return keep
             return launch, float(per), "GB/s", "hbm", "hbm", \
                 f"[{M},{N}] fp16 erf, {n} rotating buffer sets"
@@ -198,9 +208,8 @@ def kernel_cases(torch, dev):
             n = 128 << 20  # fp16 elements: 256 MB in, 256 MB out
             x = torch.ones(n, device=dev, dtype=f16)
             y = torch.empty_like(x)
-            st = s()
             keep = (x, y)
-            return (lambda i: _rc(L, lib.zk_relu(x.data_ptr(), y.data_ptr(), n, L.ZK_F16, st))
+            return (lambda i: _rc(L, lib.zk_relu(x.data_ptr(), y.data_ptr(), n, L.ZK_F16, s()))
                     and keep), float(4 * n), "GB/s", "hbm", "hbm", "256 MB read + 256 MB write"
         return setup
 
