@@ -30,6 +30,10 @@ HIPCC_FLAGS = [
     "-fPIC",
     # gfx950: keep the compiler from emitting packed fp32 instructions
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs (the unified register file allows
+    # it): no accvgpr copies between the matrix products and the VALU work
+    # on their results (softmax, epilogues)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 
