@@ -36,6 +36,15 @@ __device__ __forceinline__ int valid_len(const AttnParams &p, int b) {
   return L < 0 ? 0 : (L > p.Sk ? p.Sk : L);
 }
 
+// max(a, b, c) in one instruction. fmaxf would first quiet signalling NaNs
+// of both operands (two extra instructions per pair); scores are never
+// signalling NaNs, and -inf (masked keys) compares as usual.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 template <int D, int NW>
 __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
   constexpr int KT = 64;
@@ -127,11 +136,14 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
           if (key >= L) s[kb][r] = -__builtin_inff();
         }
     }
-    float tmax = -__builtin_inff();
+    // two independent max3 chains over the 32 scores of this lane
+    float ta = max3f(s[0][0], s[0][1], s[0][2]), tb = max3f(s[1][0], s[1][1], s[1][2]);
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) tmax = fmaxf(tmax, fmaxf(s[kb][r], s[kb][r + 1]));
+    for (int r = 3; r + 1 < 16; r += 2) {
+      ta = max3f(ta, s[0][r], s[0][r + 1]);
+      tb = max3f(tb, s[1][r], s[1][r + 1]);
+    }
+    float tmax = max3f(ta, tb, fmaxf(s[0][15], s[1][15]));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * p.scale_log2;  // finite: key t*KT < L
     // Lazy rescaling: the reference point m (log2 units) only moves when the
     // tile max exceeds it by more than 8, so exp2(s - m) <= 256 always fits
