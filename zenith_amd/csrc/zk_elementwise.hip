@@ -2,6 +2,8 @@
 // and the fp16 transpose. Every kernel moves 16-byte vectors per lane where
 // the shape and alignment allow it and falls back to a scalar grid-stride
 // loop otherwise.
+#include <type_traits>
+
 #include "zk_common.hpp"
 
 namespace zk {
@@ -54,32 +56,55 @@ static int relu_impl(const void *xv, void *yv, int64_t n, hipStream_t s) {
 }
 
 // ------------------------------------------------------------------ GELU --
-template <int MODE>
+// fp16 outputs use the branch-free forms of the GEMM epilogues (|erf error|
+// <= 1.5e-7, far below fp16's 4.9e-4 relative step), so the kernel stays
+// bound by HBM rather than by libm's erff / tanhf; fp32 keeps the exact forms.
+template <typename T, int MODE>
 __device__ __forceinline__ float gelu(float v) {
-  return MODE == ZK_GELU_ERF ? gelu_erf(v) : gelu_tanh(v);
+  if constexpr (std::is_same<T, f16>::value)
+    return MODE == ZK_GELU_ERF ? gelu_erf_fast(v) : gelu_tanh_fast(v);
+  else
+    return MODE == ZK_GELU_ERF ? gelu_erf(v) : gelu_tanh(v);
 }
 
-// One 16-byte vector per iteration; requires cols % W == 0 so a vector never
-// straddles two rows and the bias slice is contiguous.
+// Row-blocked form for cols % W == 0: a thread owns one 16-byte column
+// vector (its bias slice is loaded once) and handles kGeluRows rows per pass,
+// issuing all of their loads before any arithmetic, so that each wavefront
+// keeps kGeluRows KB in flight.
+constexpr int kGeluRows = 4;
+constexpr int kGeluBlock = 128;
+
 template <typename T, int MODE, bool BIAS>
-__global__ void gelu_vec(const T *__restrict__ x, const T *__restrict__ bias,
-                         T *__restrict__ y, int64_t nvec, int64_t cols) {
+__global__ __launch_bounds__(kGeluBlock) void gelu_rows(const T *__restrict__ x,
+                                                       const T *__restrict__ bias,
+                                                       T *__restrict__ y, int64_t rows,
+                                                       int ncv) {
   typedef typename Vec16<T>::type V;
-  constexpr int W = Vec16<T>::n;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nvec;
-       i += stride) {
-    V v = reinterpret_cast<const V *>(x)[i];
-    V b;
-    if (BIAS) b = *reinterpret_cast<const V *>(bias + (i * W) % cols);
-    V o;
+  constexpr int W = Vec16<T>::n, R = kGeluRows;
+  const int cv = blockIdx.x * kGeluBlock + threadIdx.x;
+  if (cv >= ncv) return;
+  const V *xv = reinterpret_cast<const V *>(x);
+  V *yv = reinterpret_cast<V *>(y);
+  V b;
+  if (BIAS) b = reinterpret_cast<const V *>(bias)[cv];
+  for (int64_t r0 = (int64_t)blockIdx.y * R; r0 < rows; r0 += (int64_t)gridDim.y * R) {
+    V v[R];
 #pragma unroll
-    for (int j = 0; j < W; ++j) {
-      float f = (float)v[j];
-      if (BIAS) f += (float)b[j];
-      o[j] = (T)gelu<MODE>(f);
+    for (int u = 0; u < R; ++u)
+      if (r0 + u < rows) v[u] = xv[(r0 + u) * ncv + cv];
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      if (r0 + u < rows) {
+        V o;
+#pragma unroll
+        for (int j = 0; j < W; ++j) {
+          float f = (float)v[u][j];
+          if (BIAS) f += (float)b[j];
+          o[j] = (T)gelu<T, MODE>(f);
+        }
+        yv[(r0 + u) * ncv + cv] = o;
+      }
     }
-    reinterpret_cast<V *>(y)[i] = o;
   }
 }
 
@@ -91,7 +116,7 @@ __global__ void gelu_scalar(const T *__restrict__ x, const T *__restrict__ bias,
        i += stride) {
     float f = (float)x[i];
     if (BIAS) f += (float)bias[i % cols];
-    y[i] = (T)gelu<MODE>(f);
+    y[i] = (T)gelu<T, MODE>(f);
   }
 }
 
@@ -99,11 +124,15 @@ template <typename T, int MODE, bool BIAS>
 static void gelu_launch(const T *x, const T *bias, T *y, int64_t n,
                         int64_t cols, hipStream_t s) {
   constexpr int W = Vec16<T>::n;
-  const bool vec = aligned16(x) && aligned16(y) && cols % W == 0 &&
+  const bool vec = aligned16(x) && aligned16(y) && cols % W == 0 && cols / W < (1 << 30) &&
                    (!BIAS || aligned16(bias));
-  if (vec)
-    gelu_vec<T, MODE, BIAS><<<grid_for(n / W, 256), 256, 0, s>>>(x, bias, y, n / W, cols);
-  else
+  if (vec) {
+    const int64_t rows = n / cols;
+    const int ncv = (int)(cols / W);
+    const int64_t gy = (rows + kGeluRows - 1) / kGeluRows;
+    dim3 grid((unsigned)((ncv + kGeluBlock - 1) / kGeluBlock), (unsigned)(gy > 65535 ? 65535 : gy));
+    gelu_rows<T, MODE, BIAS><<<grid, kGeluBlock, 0, s>>>(x, bias, y, rows, ncv);
+  } else
     gelu_scalar<T, MODE, BIAS><<<grid_for(n, 256), 256, 0, s>>>(x, bias, y, n, cols);
 }
 
