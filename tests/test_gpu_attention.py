@@ -125,3 +125,19 @@ def test_flash_attention_cross_lengths(dev):
     o = _run(dev, q, k, v, [150, 200], torch.float16)
     ok, worst = fp16_tol(o, ops.attention(q, k, v, np.array([150, 200])))
     assert ok, worst
+
+
+@pytest.mark.parametrize("S", [128, 512])
+def test_flash_attention_deterministic(dev, S):
+    """Repeated launches on the same inputs give bit-identical outputs (the
+    kernel has no atomics or reduction-order freedom; a difference means a
+    read racing a write or a missing wait on a matrix-core result)."""
+    from zenith_amd import zenith_cuda as zc
+
+    B, H, D = 8, 12, 64
+    q, k, v = (torch.from_numpy(a).to(dev, torch.float16) for a in _qkv(B, H, S, S, D, tag=90))
+    lens = torch.from_numpy(synthetic.padding_lengths(B, S, seed=9)).to(dev)
+    first = zc.flash_attention(q, k, v, key_padding_lengths=lens)
+    for _ in range(5):
+        again = zc.flash_attention(q, k, v, key_padding_lengths=lens)
+        assert torch.equal(again, first)

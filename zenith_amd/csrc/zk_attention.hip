@@ -2,7 +2,8 @@
 //
 // fp16 path (MFMA). A workgroup of NW wavefronts owns NW*32 query rows of
 // one (batch, head); every wavefront owns 32 of them. Keys are walked in
-// tiles of 64: K is staged in LDS as [key][d] and V transposed as [d][key].
+// tiles of 64: K and V are staged in LDS as [key][d] with 16-byte stores; the
+// V^T fragments of the P.V product come out of the transposing LDS read.
 // The wavefront computes S^T = K . Q^T with 32x32x16 MFMAs, so each lane
 // ends up holding 32 keys of ONE query column (lane % 32): the row max and
 // row sum of the online softmax are then a register loop plus a single
@@ -36,26 +37,25 @@ __device__ __forceinline__ int valid_len(const AttnParams &p, int b) {
   return L < 0 ? 0 : (L > p.Sk ? p.Sk : L);
 }
 
-// max(a, b, c) in one instruction. fmaxf would first quiet signalling NaNs
-// of both operands (two extra instructions per pair); scores are never
-// signalling NaNs, and -inf (masked keys) compares as usual.
-__device__ __forceinline__ float max3f(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
+// ds_read_b64_tr_b16: 8 bytes per lane, transposed across each group of 16
+// lanes (see its use below for the lane mapping).
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f16x4 lds_read_tr16(const f16 *p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4 *)(p));
+  return __builtin_bit_cast(f16x4, v);
 }
 
 template <int D, int NW>
 __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
   constexpr int KT = 64;
   constexpr int NT = NW * 64;
-  constexpr int KLD = D + 8;   // K tile row pitch (halves)
-  constexpr int VLD = KT + 4;  // V^T tile row pitch (halves)
+  constexpr int KLD = D + 8;   // K and V tile row pitch (halves)
   constexpr int DV = D / 8;    // 16-byte vectors per K/V row
   constexpr int PER = KT * DV / NT;
   static_assert(KT * DV % NT == 0, "tile/thread mismatch");
   __shared__ __attribute__((aligned(16))) f16 Ks[KT * KLD];
-  __shared__ __attribute__((aligned(16))) f16 Vt[D * VLD];
+  __shared__ __attribute__((aligned(16))) f16 Vs[KT * KLD];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h32 = lane >> 5;
   const int b = blockIdx.z, h = blockIdx.y;
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
       const int kk = t * KT + idx / DV;  // K: 16-byte vectors row-contiguous
       kr[v] = kk < p.Sk ? *(const f16x8 *)(Kb + kk * p.sk[2] + (idx % DV) * 8)
                         : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      // V like K (8 lanes per 128-byte row, coalesced); transposed when stored.
+      // V like K (8 lanes per 128-byte row, coalesced)
       vr[v] = kk < p.Sk ? *(const f16x8 *)(Vb + kk * p.sv[2] + (idx % DV) * 8)
                         : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
     }
@@ -99,9 +99,7 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
     for (int v = 0; v < PER; ++v) {
       const int idx = tid + v * NT;
       *(f16x8 *)(Ks + (idx / DV) * KLD + (idx % DV) * 8) = kr[v];
-      const int key = idx / DV, d0 = (idx % DV) * 8;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) Vt[(d0 + j) * VLD + key] = vr[v][j];
+      *(f16x8 *)(Vs + (idx / DV) * KLD + (idx % DV) * 8) = vr[v];
     }
   };
 
@@ -136,14 +134,11 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
           if (key >= L) s[kb][r] = -__builtin_inff();
         }
     }
-    // two independent max3 chains over the 32 scores of this lane
-    float ta = max3f(s[0][0], s[0][1], s[0][2]), tb = max3f(s[1][0], s[1][1], s[1][2]);
+    float tmax = -__builtin_inff();
 #pragma unroll
-    for (int r = 3; r + 1 < 16; r += 2) {
-      ta = max3f(ta, s[0][r], s[0][r + 1]);
-      tb = max3f(tb, s[1][r], s[1][r + 1]);
-    }
-    float tmax = max3f(ta, tb, fmaxf(s[0][15], s[1][15]));
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) tmax = fmaxf(tmax, fmaxf(s[kb][r], s[kb][r + 1]));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * p.scale_log2;  // finite: key t*KT < L
     // Lazy rescaling: the reference point m (log2 units) only moves when the
     // tile max exceeds it by more than 8, so exp2(s - m) <= 256 always fits
@@ -173,16 +168,23 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
     l += psum;
     // O^T[d][q] += V^T[d][key] . P^T[key][q], 16 keys per MFMA. Lane-half
     // h32, slot j of the P^T fragment holds key 16*c2 + 8*(j/4) + 4*h32 +
-    // j%4 of block kb; the V^T fragment is read with the same key order.
+    // j%4 of block kb; the V^T fragment (lane l: dim l % 32 of block dt, the
+    // same keys) comes from the row-major V tile through the transposing LDS
+    // read: in each group of 16 lanes, output lane i, slot j receives element
+    // i % 4 of the 4 elements read by source lane 4*j + i/4. Source lane s
+    // therefore reads key k0 + s/4, dims dbase + 4*(s%4), and output lane i
+    // gets dim dbase + i at keys k0 .. k0+3.
+    const int grp = lane >> 4, sl = lane & 15;
+    const f16 *vsrc = Vs + (4 * (grp >> 1) + (sl >> 2)) * KLD + 16 * (grp & 1) + 4 * (sl & 3);
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2) {
-          const f16 *vrow = Vt + (dt * 32 + (lane & 31)) * VLD + kb * 32 + c2 * 16 + 4 * h32;
-          const f16x4 lo = *(const f16x4 *)vrow;
-          const f16x4 hi = *(const f16x4 *)(vrow + 8);
+          const f16 *src = vsrc + (kb * 32 + c2 * 16) * KLD + dt * 32;
+          const f16x4 lo = lds_read_tr16(src);
+          const f16x4 hi = lds_read_tr16(src + 8 * KLD);
           const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
           o[dt] = mfma32x32x16(vf, pf[kb][c2], o[dt]);
         }
