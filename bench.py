@@ -18,6 +18,9 @@ replayed from a HIP graph, inputs resident in HBM. Prints ONE JSON line with:
                        attention s128 / s512 (config 3), INT8 FFN GEMMs
                        (config 4), Add+LayerNorm and bias+GELU (HBM, buffer
                        sets rotated past the 256 MB MALL)
+  e4_hybrid            the reference's published BERT comparator workload
+                       (hybrid encoder on the GpuTensor API, b1 s128, timed
+                       as the reference times it) beside its 9.74 ms (T4)
   cpu_baseline         the CPU oracle (numpy fp32 restatement of the
                        reference's CPU path) on a bounded sample of the same
                        workload (whole sequences through 12 layers)
@@ -58,6 +61,7 @@ def _args():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-int8", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
+    ap.add_argument("--no-e4", action="store_true", help="skip the hybrid-API encoder (E4)")
     ap.add_argument("--only", default=None, help="launch one kernel --iters times and exit")
     ap.add_argument("--iters", type=int, default=20)
     return ap.parse_args()
@@ -281,6 +285,42 @@ def pmc_traffic():
     return float(m.group(1)) if m else None
 
 
+# ----------------------------------------------------- E4 hybrid encoder --
+E4_PUBLISHED_MS = 9.74  # T4, BENCHMARK_REPORT.md:54 (benchmarks/bert_hybrid.py:171-273)
+
+
+def e4_hybrid(torch, runs: int = 50, warmup: int = 5):
+    """The reference's published BERT comparator on its own API: the hybrid
+    encoder (fp32 linears, fp16 attention; 12 layers, b=1, s=128) written
+    against the GpuTensor API, timed as the reference times it: host clock
+    around one eager forward plus a device sync, mean over `runs` after
+    `warmup` (bert_hybrid.py:233-251). Eager launches from Python included."""
+    import numpy as np
+
+    from zenith_amd import core_cuda as cuda
+    from zenith_amd import synthetic
+    from zenith_amd.bert_hybrid import BertEncoderHybrid
+
+    B, S = 1, 128
+    enc = BertEncoderHybrid(12).load_weights(synthetic.bert_weights(12))
+    x = cuda.to_gpu(synthetic.hidden_states(B, S).reshape(B * S, 768))
+    for _ in range(warmup):
+        enc.forward(x, B, S)
+    cuda.sync()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        out = enc.forward(x, B, S)
+        cuda.sync()
+        times.append((time.perf_counter() - t0) * 1e3)
+    assert np.isfinite(out.to_numpy()).all(), "non-finite hybrid output"
+    ms = float(np.mean(times))
+    return {"workload": "BERT-base 12-layer hybrid encoder (GpuTensor API), b1 s128, fp32 linears "
+                        "+ fp16 attention, eager", "ms": round(ms, 3), "std_ms": round(float(np.std(times)), 3),
+            "seqs_per_s": round(1e3 / ms, 1), "published_ms": E4_PUBLISHED_MS,
+            "published_hw": "T4", "vs_published": round(E4_PUBLISHED_MS / ms, 2)}
+
+
 # ---------------------------------------------------------- CPU baseline --
 def cpu_baseline(seq: int, layers: int, budget_s: float):
     """Oracle fp32 encoder on whole sequences until the time budget is used."""
@@ -398,6 +438,7 @@ def main():
     del enc
     torch.cuda.empty_cache()
 
+    e4 = None if args.no_e4 else e4_hybrid(torch)
     roof = measure_kernels(torch, dev, ["gemm_ffn_up"])[0]
     kernels = None if args.no_kernels else measure_kernels(torch, dev)
     cpu = None if args.no_cpu else cpu_baseline(S, args.layers, args.cpu_seconds)
@@ -417,6 +458,7 @@ def main():
         "roofline_kernel": {"kernel": "gemm_mfma_kernel<F16, bias+gelu_erf> M=4096 K=768 N=3072",
                             "avg_launch_us": roof["us"], "flops_per_launch": 2.0 * 4096 * 768 * 3072},
         "kernels": kernels,
+        "e4_hybrid": e4,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -109,7 +109,9 @@ int zk_gemm_f16(const void *A, const void *B, void *C, int64_t M, int64_t N,
                 int out_dtype, const void *bias, const void *residual,
                 int64_t ldr, int epilogue, void *stream);
 
-/* FP32 GEMM, C[M,N] = A[M,K] . op(B), trans_b as above, fp32 throughout.
+/* FP32 GEMM, C[M,N] = A[M,K] . op(B), trans_b as above, fp32 throughout
+ * (with trans_b and 16-byte aligned rows, K % 4 == 0: fp32 MFMA products
+ * with fp32 accumulation; otherwise the SIMT kernel).
  * Replaces zenith_cuda.matmul (cuda_bindings.cpp:73-88 ->
  * matmul_f32 cuda_kernels.cu:297-336, 524-528). */
 int zk_gemm_f32(const float *A, const float *B, float *C, int64_t M,
@@ -168,6 +170,36 @@ int zk_gemm_i8_requant(const int8_t *A, const int8_t *W, int8_t *Q, int64_t M,
                        int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldq,
                        float s_x, const float *s_w, const void *bias, int epilogue,
                        float s_out, void *stream);
+
+/* c[r, :] = a[r, :] + b[b_rows == 1 ? 0 : r, :] for [rows, cols] contiguous
+ * tensors in dtype ZK_F32 or ZK_F16 (fp16 summed in fp32, rounded once);
+ * b_rows is 1 (row broadcast: bias) or rows.
+ * Replaces add_2d_f32 and add_bias_f32 (core/src/cuda_kernels.cu:582-616)
+ * and add_fp16 (core/src/fp16_kernels.cu:267-280). */
+int zk_add(const void *a, const void *b, void *c, int64_t rows, int64_t cols,
+           int64_t b_rows, int dtype, void *stream);
+
+/* Row softmax y = exp(x - max) / sum over the last dim of [rows, cols]
+ * contiguous, fp32 math (exact expf), dtype ZK_F32 or ZK_F16.
+ * Replaces softmax_2d_f32 (core/src/cuda_kernels.cu:220-246, 577-580; CPU
+ * form softmax_f32, core/src/cpu_kernels.cpp:382-408). */
+int zk_softmax(const void *x, void *y, int64_t rows, int64_t cols, int dtype,
+               void *stream);
+
+/* y[i][k][j][l] = x[i][j][k][l] for contiguous x of shape [d0, d1, d2, d3]
+ * (attention head split / merge: [B,S,H,D] <-> [B,H,S,D]), dtype ZK_F32
+ * or ZK_F16, not in place.
+ * Replaces transpose_0213_f32 / transpose_0213_inv_f32
+ * (core/src/cuda_kernels.cu:623-678) and their fp16 twins
+ * (core/src/fp16_kernels.cu:285-325). */
+int zk_transpose_0213(const void *x, void *y, int64_t d0, int64_t d1, int64_t d2,
+                      int64_t d3, int dtype, void *stream);
+
+/* n-element conversion between ZK_F32 and ZK_F16 (round to nearest even).
+ * Replaces convert_f32_to_f16 / convert_f16_to_f32
+ * (core/src/fp16_kernels.cu:50-77) and convert_fp32_to_fp16 (fp16_ops.cu:56). */
+int zk_convert(const void *x, void *y, int64_t n, int src_dtype, int dst_dtype,
+               void *stream);
 
 #ifdef __cplusplus
 }

@@ -140,6 +140,33 @@ def test_matmul_fp32(dev, M, K, N):
     np.testing.assert_allclose(c.cpu().numpy(), ops.matmul_f64(a, b), rtol=1e-5, atol=1e-4)
 
 
+@pytest.mark.parametrize("M,K,N", [
+    (4100, 72, 4100),   # 8-wave 256x256 tile
+    (4000, 100, 2000),  # 8-wave 256x192 tile
+    (520, 200, 20500),  # 128x128, 2-stage ring
+    (700, 136, 1100),   # 128x96, 16x16x4 fp32 MFMA
+    (1000, 3000, 600),  # 128x128, 3-stage ring
+    (333, 500, 1000),   # 64x64
+    (128, 768, 3072),   # the hybrid encoder's FFN-up shape
+    (77, 70, 33),       # K % 4 != 0: the SIMT kernel
+])
+def test_linear_fp32_tile_configs(dev, M, K, N):
+    """fp32 Linear through the fp32-MFMA GEMM (every tile configuration, at
+    ragged edges) and the SIMT fallback, vs the float64 product."""
+    from zenith_amd import zenith_cuda as zc
+
+    x = synthetic.normal((M, K), tag=40)
+    w = synthetic.normal((N, K), tag=41, std=0.05)
+    b = synthetic.normal((N,), tag=42)
+    y = zc.linear(_t(x, dev, torch.float32), _t(w, dev, torch.float32), _t(b, dev, torch.float32))
+    rows = np.random.default_rng(M).choice(M, min(M, 256), replace=False)
+    rows.sort()
+    ref = ops.matmul_f64(x[rows], w.T) + b
+    got = y[torch.from_numpy(rows).to(dev)].cpu().numpy()
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(y[-2:].cpu().numpy(), ops.matmul_f64(x[-2:], w.T) + b, rtol=1e-4, atol=1e-4)
+
+
 def test_linear_fp32(dev):
     from zenith_amd import zenith_cuda as zc
 

@@ -97,6 +97,11 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
   return v;
 }
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
 
 // ------------------------------------------------------------------ MFMA --
 // D(32x32, fp32) += A(32x16, f16) . B(16x32, f16). Lane l supplies

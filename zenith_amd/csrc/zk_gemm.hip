@@ -100,10 +100,42 @@ template <> struct I8Mma<16> {
   }
 };
 
+// fp32 on the matrix cores: 16 bytes per lane and operand are four fp32
+// values, k0 + 4 * (lane slot) + j, consumed by four chained fp32 MFMAs in
+// which element j of every lane is the operand (32x32x2: lane half = k
+// index; 16x16x4: lane quarter = k index). The four products together cover
+// the same 8 (MS = 32) or 16 (MS = 16) consecutive k as one fp16 step.
+template <int MS> struct F32Mma;
+template <> struct F32Mma<32> {
+  typedef f32x16 Acc;
+  static constexpr int R = 16;
+  static __device__ __forceinline__ Acc mma(f32x4 a, f32x4 b, Acc c) {
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[0], b[0], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[1], b[1], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[2], b[2], c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a[3], b[3], c, 0, 0, 0);
+  }
+};
+template <> struct F32Mma<16> {
+  typedef f32x4 Acc;
+  static constexpr int R = 4;
+  static __device__ __forceinline__ Acc mma(f32x4 a, f32x4 b, Acc c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], b[0], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], b[1], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], b[2], c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a[3], b[3], c, 0, 0, 0);
+  }
+};
+
 struct F16Op {
   typedef f16x8 Frag;
   template <int MS> using Mma = F16Mma<MS>;
   static constexpr int kElem = 2;
+};
+struct F32Op {
+  typedef f32x4 Frag;
+  template <int MS> using Mma = F32Mma<MS>;
+  static constexpr int kElem = 4;
 };
 struct I8Op {
   typedef i32x4 Frag;
@@ -728,9 +760,18 @@ extern "C" int zk_gemm_f32(const float *A, const float *B, float *C, int64_t M,
   if (!A || !B || !C) return fail(ZK_ERR_INVALID, "zk_gemm_f32: null pointer");
   if (lda < K || ldc < N || (trans_b ? ldb < K : ldb < N))
     return fail(ZK_ERR_INVALID, "zk_gemm_f32: leading dimension too small");
+  hipStream_t s = as_stream(stream);
+  // W[N,K] operand with 16-byte rows: the MFMA kernel (fp32 matrix-core
+  // products, fp32 accumulation); buffer offsets of a 256-row tile must fit
+  // in 31 bits.
+  if (trans_b && K > 0 && K % 4 == 0 && lda % 4 == 0 && ldb % 4 == 0 && aligned16(A) &&
+      aligned16(B) && lda < (1 << 21) && ldb < (1 << 21)) {
+    GemmParams p{A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc, nullptr, nullptr, 0, 1.f, nullptr, 0};
+    launch_mfma<F32Op, float, false>(p, ZK_EPI_NONE, s);
+    return check_launch("zk_gemm_f32");
+  }
   if ((M + 63) / 64 > 65535) return fail(ZK_ERR_UNSUPPORTED, "zk_gemm_f32: M too large");
   dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
-  hipStream_t s = as_stream(stream);
   if (trans_b)
     gemm_f32_kernel<true><<<grid, 256, 0, s>>>(A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc);
   else

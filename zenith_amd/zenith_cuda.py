@@ -312,13 +312,16 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
             y = bias_gelu(y, bias.contiguous(),
                           approximate="tanh" if activation == "gelu_tanh" else "none")
         else:
-            y = y + bias
+            if M:
+                L.call("zk_add", _p(y), _p(bias.to(torch.float32).contiguous()), _p(y), M, N, 1,
+                       L.ZK_F32, _stream(y))
             if activation == "relu":
                 y = relu(y)
     elif activation is not None:
         y = gelu(y, "tanh" if activation == "gelu_tanh" else "none") if activation != "relu" else relu(y)
-    if residual is not None:
-        y = y + residual.reshape(-1, N)
+    if residual is not None and M:
+        r = residual.reshape(-1, N).to(torch.float32).contiguous()
+        L.call("zk_add", _p(y), _p(r), _p(y), M, N, M, L.ZK_F32, _stream(y))
     return y.reshape(*lead, N)
 
 
