@@ -201,6 +201,30 @@ int zk_transpose_0213(const void *x, void *y, int64_t d0, int64_t d1, int64_t d2
 int zk_convert(const void *x, void *y, int64_t n, int src_dtype, int dst_dtype,
                void *stream);
 
+/* Workspace for the split-K form of the GEMMs: bytes zk_gemm_f16_ws /
+ * zk_gemm_f32_ws (dtype ZK_F16 / ZK_F32) use for an M x N x K product, 0 when
+ * the product is not split. Small-M products (too few 64x64 tiles to fill
+ * the GPU) are split along K; each split writes an fp32 partial tile to the
+ * workspace and a reduction sums the splits in order (deterministic) and
+ * applies the epilogue. The workspace is the caller's (the library
+ * allocates nothing); no counterpart in the reference, whose
+ * cuBLAS calls hid their own workspaces (python/src/bindings.cpp:1454-1498). */
+int64_t zk_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int dtype);
+
+/* zk_gemm_f16 with a caller workspace of ws_bytes (see
+ * zk_gemm_workspace_size); with a null or too small workspace it is
+ * zk_gemm_f16. */
+int zk_gemm_f16_ws(const void *A, const void *B, void *C, int64_t M, int64_t N,
+                   int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_b,
+                   int out_dtype, const void *bias, const void *residual, int64_t ldr,
+                   int epilogue, void *workspace, int64_t ws_bytes, void *stream);
+
+/* zk_gemm_f32 with a caller workspace of ws_bytes (split-K on the fp32
+ * MFMA path); with a null or too small workspace it is zk_gemm_f32. */
+int zk_gemm_f32_ws(const float *A, const float *B, float *C, int64_t M, int64_t N,
+                   int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_b,
+                   void *workspace, int64_t ws_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

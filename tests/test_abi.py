@@ -85,3 +85,17 @@ def test_c_types_are_plain():
         for a in args:
             assert a in (ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float) or \
                 a is ctypes.POINTER(ctypes.c_int64), (name, a)
+
+
+def test_gemm_workspace_plan():
+    """Split-K workspace sizes: small-M products are split (fp32 partials of
+    M x N per split), large ones are not; pure host logic, no GPU."""
+    from zenith_amd import _lib as L
+
+    lib = L.load()
+    ws = lib.zk_gemm_workspace_size(128, 768, 3072, L.ZK_F32)
+    assert ws > 0 and ws % (128 * 768 * 4) == 0 and 2 <= ws // (128 * 768 * 4) <= 16
+    assert lib.zk_gemm_workspace_size(4096, 768, 3072, L.ZK_F32) == 0
+    assert lib.zk_gemm_workspace_size(4096, 3072, 768, L.ZK_F16) == 0
+    assert lib.zk_gemm_workspace_size(64, 64, 64, L.ZK_F16) == 0  # too few K slices
+    assert lib.zk_gemm_workspace_size(0, 768, 768, L.ZK_F32) == 0

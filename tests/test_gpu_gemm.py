@@ -176,3 +176,41 @@ def test_linear_fp32(dev):
     y = zc.linear(_t(x, dev, torch.float32), _t(w, dev, torch.float32), _t(b, dev, torch.float32),
                   activation="gelu")
     np.testing.assert_allclose(y.cpu().numpy(), ops.gelu_erf(ops.linear(x, w, b)), rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("M,K,N", [(128, 3072, 768), (128, 768, 768), (37, 1000, 200), (128, 768, 3072)])
+@pytest.mark.parametrize("act", [None, "gelu", "residual"])
+def test_linear_split_k(dev, M, K, N, act):
+    """Small-M products take the split-K path (caller workspace, fp32
+    partials, ordered reduction with the epilogue): fp16 and fp32, against
+    the float64 product, and bit-identical on repeated calls."""
+    from zenith_amd import _lib as L
+    from zenith_amd import zenith_cuda as zc
+
+    assert L.load().zk_gemm_workspace_size(M, N, K, L.ZK_F32) > 0
+    x = synthetic.normal((M, K), tag=50)
+    w = synthetic.normal((N, K), tag=51, std=0.03)
+    b = synthetic.normal((N,), tag=52, std=0.5)
+    r = synthetic.normal((M, N), tag=53)
+    ref = ops.matmul_f64(x, w.T) + b
+    if act == "gelu":
+        ref = ops.gelu_erf(ref.astype(np.float32))
+    elif act == "residual":
+        ref = ref + r
+    kw = dict(activation="gelu" if act == "gelu" else None)
+    y32 = zc.linear(_t(x, dev, torch.float32), _t(w, dev, torch.float32), _t(b, dev, torch.float32),
+                    residual=_t(r, dev, torch.float32) if act == "residual" else None, **kw)
+    np.testing.assert_allclose(y32.cpu().numpy(), ref, rtol=1e-4, atol=1e-4)
+    x16, w16, b16, r16 = (synthetic.round_f16(a) for a in (x, w, b, r))
+    ref16 = ops.matmul_f64(x16, w16.T) + b16
+    if act == "gelu":
+        ref16 = ops.gelu_erf(ref16.astype(np.float32))
+    elif act == "residual":
+        ref16 = ref16 + r16
+    args = (_t(x16, dev, torch.float16), _t(w16, dev, torch.float16), _t(b16, dev, torch.float16))
+    res = _t(r16, dev, torch.float16) if act == "residual" else None
+    y16 = zc.linear(*args, residual=res, **kw)
+    ok, worst = fp16_tol(y16.float().cpu().numpy(), ref16)
+    assert ok, worst
+    for _ in range(3):
+        assert torch.equal(zc.linear(*args, residual=res, **kw), y16)

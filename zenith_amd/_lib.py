@@ -53,12 +53,16 @@ SIGNATURES: dict[str, list] = {
                    _vp, _vp, _i64, _i32, _i32, _vp],
     "zk_gemm_i8_requant": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _vp,
                            _vp, _i32, _f32, _vp],
+    "zk_gemm_workspace_size": [_i64, _i64, _i64, _i32],
+    "zk_gemm_f16_ws": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
+                       _vp, _vp, _i64, _i32, _vp, _i64, _vp],
+    "zk_gemm_f32_ws": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _vp, _i64, _vp],
     "zk_add": [_vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
     "zk_softmax": [_vp, _vp, _i64, _i64, _i32, _vp],
     "zk_transpose_0213": [_vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp],
     "zk_convert": [_vp, _vp, _i64, _i32, _i32, _vp],
 }
-_RESTYPES = {"zk_last_error": ctypes.c_char_p}
+_RESTYPES = {"zk_last_error": ctypes.c_char_p, "zk_gemm_workspace_size": ctypes.c_int64}
 
 _lock = threading.Lock()
 _lib = None

@@ -30,6 +30,7 @@ import numpy as np
 import torch
 
 from . import _lib as L
+from .zenith_cuda import _pad_k, _ws_args, gemm_workspace
 
 F32, F16 = torch.float32, torch.float16
 
@@ -213,7 +214,9 @@ def linear_gpu(X: GpuTensor, W: GpuTensor, bias: GpuTensor) -> GpuTensor:
         raise RuntimeError("linear_gpu: W.dim(1) must match X.dim(1)")
     y = _new(x, (M, N))
     s = _stream(x)
-    L.call("zk_gemm_f32", x.data_ptr(), w.data_ptr(), y.data_ptr(), M, N, K, K, K, N, 1, s)
+    ws = gemm_workspace(M, N, K, L.ZK_F32, x.device)
+    L.call("zk_gemm_f32_ws", x.data_ptr(), w.data_ptr(), y.data_ptr(), M, N, K, K, K, N, 1,
+           *_ws_args(ws), s)
     if isinstance(bias, GpuTensor) and bias.is_valid() and bias.dim(0) == N:
         L.call("zk_add", y.data_ptr(), bias.tensor.data_ptr(), y.data_ptr(), M, N, 1, L.ZK_F32, s)
     return GpuTensor(y)
@@ -341,9 +344,12 @@ def linear_fp16_gpu(X: GpuTensor, W: GpuTensor, bias: GpuTensor) -> GpuTensor:
     x16, w16 = _to16(x), _to16(w)
     b16 = _to16(bias.tensor) if has_bias else None
     y16 = _new(x, (M, N), F16)
-    L.call("zk_gemm_f16", x16.data_ptr(), w16.data_ptr(), y16.data_ptr(), M, N, K, K, K, N, 1,
+    x16, w16 = _pad_k(x16, 8), _pad_k(w16, 8)  # zero columns: K a multiple of 8
+    K = x16.shape[1]
+    ws = gemm_workspace(M, N, K, L.ZK_F16, x.device)
+    L.call("zk_gemm_f16_ws", x16.data_ptr(), w16.data_ptr(), y16.data_ptr(), M, N, K, K, K, N, 1,
            L.ZK_F16, None if b16 is None else b16.data_ptr(), None, 0,
-           L.ZK_EPI_BIAS if has_bias else L.ZK_EPI_NONE, _stream(x))
+           L.ZK_EPI_BIAS if has_bias else L.ZK_EPI_NONE, *_ws_args(ws), _stream(x))
     return _to32(y16)
 
 

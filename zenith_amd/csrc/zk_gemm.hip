@@ -60,6 +60,12 @@ struct GemmParams {
   int tiles_m;
   int group_m;
   float s_q;  // int8 output: scale of the re-quantisation
+  // split-K: workgroup (tile t, split s) = blockIdx t * splits + s covers K
+  // slices [s * nk_per, +nk_per) and writes its fp32 partial tile to
+  // C + s * split_stride (C is then the workspace, ldc = N)
+  int splits;
+  int nk_per;
+  int64_t split_stride;
 };
 
 #define ZK_LDS(p) ((__attribute__((address_space(3))) void *)(p))
@@ -276,7 +282,13 @@ void gemm_mfma_kernel(GemmParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
   const int wm = wave / WN, wn = wave % WN;
   int tm, tn;
-  tile_of(blockIdx.x, gridDim.x, p, tm, tn);
+  int split = 0, twg = blockIdx.x, nwg = gridDim.x;
+  if (p.splits > 1) {
+    split = blockIdx.x % p.splits;
+    twg = blockIdx.x / p.splits;
+    nwg = gridDim.x / p.splits;
+  }
+  tile_of(twg, nwg, p, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int kbytes = p.K * OP::kElem;
   const int64_t lda_b = p.lda * OP::kElem, ldb_b = p.ldb * OP::kElem;
@@ -344,7 +356,9 @@ void gemm_mfma_kernel(GemmParams p) {
       for (int j = 0; j < TN; ++j) acc[i][j] = MM::mma(fa[buf][i], fb[buf][j], acc[i][j]);
   };
 
-  const int nk = (kbytes + BKB - 1) / BKB;
+  const int nk_all = (kbytes + BKB - 1) / BKB;
+  const int kt0 = p.splits > 1 ? split * p.nk_per : 0;  // first slice of this split
+  const int nk = p.splits > 1 ? max(0, min(nk_all - kt0, p.nk_per)) : nk_all;
   // One K slice of A and W: IA + IB wavefront instructions, each moving
   // 1 KB (64 lanes x 16 bytes) into consecutive LDS bytes. The host
   // compilation pass sees an empty statement: its semantic check of this
@@ -353,7 +367,7 @@ void gemm_mfma_kernel(GemmParams p) {
 #if defined(__HIP_DEVICE_COMPILE__)
 #define ZK_ISSUE(kt, stage)                                                                   \
   do {                                                                                        \
-    const int kb_ = (kt) * BKB;                                                               \
+    const int kb_ = ((kt) + kt0) * BKB;                                                       \
     char *as_ = smem + (stage) * G::STAGE, *bs_ = as_ + BM * BKB;                             \
     _Pragma("unroll") for (int g = 0; g < IA; ++g)                                            \
         __builtin_amdgcn_raw_ptr_buffer_load_lds(                                             \
@@ -412,7 +426,7 @@ void gemm_mfma_kernel(GemmParams p) {
   // rounded to fp16 first, so the result equals quantising the fp16 output.
   constexpr bool Q8 = std::is_same<OutT, int8_t>::value;
   typedef typename std::conditional<Q8, f16, OutT>::type BiasT;
-  OutT *C = (OutT *)p.C;
+  OutT *C = (OutT *)p.C + (p.splits > 1 ? split * p.split_stride : 0);
   const BiasT *bias = (const BiasT *)p.bias;
   const BiasT *res = (const BiasT *)p.res;
   const float inv_q = Q8 ? 1.0f / p.s_q : 1.0f;
@@ -523,7 +537,7 @@ template <class OP, int BM, int BN, int MS, int BKB, int ST, typename OutT, bool
 static void launch_epi(GemmParams p, int epi, hipStream_t s) {
   p.tiles_n = (p.N + BN - 1) / BN;
   p.tiles_m = (p.M + BM - 1) / BM;
-  const int grid = p.tiles_m * p.tiles_n;
+  const int grid = p.tiles_m * p.tiles_n * (p.splits > 1 ? p.splits : 1);
   // tile rows per group: enough that one XCD's share of the grid is a
   // rectangle about as tall as it is wide
   int gm = 1;
@@ -555,13 +569,17 @@ static void launch_epi(GemmParams p, int epi, hipStream_t s) {
 //     8-wave 256x192 tile;
 //   otherwise 128x128 once that gives >= 640 tiles, else 128x96.
 // ZK_GEMM_CFG=<id> forces a configuration (tuning runs).
-static int pick_cfg(int M, int N, int K) {
+static int forced_cfg() {
   static int forced = -2;
   if (forced == -2) {
     const char *e = getenv("ZK_GEMM_CFG");
     forced = e ? atoi(e) : -1;
   }
-  if (forced >= 0 && forced < kNumCfgs) return forced;
+  return forced >= 0 && forced < kNumCfgs ? forced : -1;
+}
+
+static int pick_cfg(int M, int N, int K) {
+  if (forced_cfg() >= 0) return forced_cfg();
   const int64_t tm256 = (M + 255) / 256;
   if (M >= 1024 && N > 1024 && tm256 * ((N + 255) / 256) >= 256) return 0;
   if (N <= 1024) return K >= 2048 ? 4 : 3;
@@ -571,8 +589,8 @@ static int pick_cfg(int M, int N, int K) {
 }
 
 template <class OP, typename OutT, bool DEQ>
-static void launch_mfma(GemmParams p, int epi, hipStream_t s) {
-  switch (pick_cfg(p.M, p.N, p.K)) {
+static void launch_mfma(GemmParams p, int epi, hipStream_t s, int cfg = -1) {
+  switch (cfg >= 0 ? cfg : pick_cfg(p.M, p.N, p.K)) {
     case 0: launch_epi<OP, 256, 256, 32, 128, 2, OutT, DEQ, 2, 4>(p, epi, s); break;
     case 1: launch_epi<OP, 128, 128, 32, 128, 2, OutT, DEQ>(p, epi, s); break;
     case 2: launch_epi<OP, 128, 96, 16, 128, 2, OutT, DEQ>(p, epi, s); break;
@@ -580,6 +598,86 @@ static void launch_mfma(GemmParams p, int epi, hipStream_t s) {
     case 5: launch_epi<OP, 256, 192, 32, 128, 2, OutT, DEQ, 4, 2>(p, epi, s); break;
     default: launch_epi<OP, 64, 64, 16, 128, 2, OutT, DEQ>(p, epi, s); break;
   }
+}
+
+// --------------------------------------------------------------- split-K --
+// Problems whose 64x64 tiles cannot fill the GPU (small M, e.g. one
+// sequence of 128 tokens) are split along K: workgroup (tile, split) runs
+// the 64x64 kernel over its K range and writes the raw fp32 partial tile to
+// a caller-provided workspace; splitk_reduce then sums the partials in split
+// order (deterministic) and applies the epilogue.
+struct SplitPlan {
+  int splits;  // 1: no split
+  int nk_per;  // 128-byte K slices per split
+};
+
+static SplitPlan plan_split(int64_t M, int64_t N, int64_t K, int elem) {
+  SplitPlan sp{1, 0};
+  if (forced_cfg() >= 0) return sp;
+  const int64_t t64 = ((M + 63) / 64) * ((N + 63) / 64);
+  const int64_t nk_all = (K * elem + 127) / 128;
+  if (t64 >= 128 || nk_all < 4) return sp;
+  int64_t splits = 256 / t64;
+  if (splits > 16) splits = 16;
+  if (splits > nk_all / 2) splits = nk_all / 2;
+  if (splits < 2) return sp;
+  const int64_t per = (nk_all + splits - 1) / splits;
+  splits = (nk_all + per - 1) / per;  // no empty split
+  if (splits < 2) return sp;
+  return SplitPlan{(int)splits, (int)per};
+}
+
+static int64_t split_ws_bytes(int64_t M, int64_t N, const SplitPlan &sp) {
+  return sp.splits > 1 ? (int64_t)sp.splits * M * N * (int64_t)sizeof(float) : 0;
+}
+
+template <int EPI, typename OutT>
+__global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ ws, int splits,
+                                                     int64_t stride, int M, int N,
+                                                     const OutT *__restrict__ bias,
+                                                     const OutT *__restrict__ res, int64_t ldr,
+                                                     OutT *__restrict__ C, int64_t ldc) {
+  const int64_t total = (int64_t)M * N;
+  const int64_t step = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += step) {
+    const int64_t m = i / N, n = i % N;
+    float v = 0.f;
+    for (int sp = 0; sp < splits; ++sp) v += ws[sp * stride + i];
+    v = epilogue<EPI>(v, EPI != ZK_EPI_NONE ? to_f(bias[n]) : 0.f);
+    if (EPI == ZK_EPI_BIAS_RESIDUAL) v += to_f(res[m * ldr + n]);
+    C[m * ldc + n] = (OutT)v;
+  }
+}
+
+// p describes the final product (C, ldc, bias, residual); the partials go to
+// ws (at least split_ws_bytes). OP is F16Op or F32Op.
+template <class OP, typename OutT>
+static void launch_split(GemmParams p, int epi, const SplitPlan &sp, float *ws, hipStream_t s) {
+  GemmParams q = p;
+  q.C = ws;
+  q.ldc = p.N;
+  q.bias = nullptr;
+  q.res = nullptr;
+  q.splits = sp.splits;
+  q.nk_per = sp.nk_per;
+  q.split_stride = (int64_t)p.M * p.N;
+  launch_mfma<OP, float, false>(q, ZK_EPI_NONE, s, 3);
+  const int64_t total = (int64_t)p.M * p.N;
+  int64_t g = (total + 255) / 256;
+  if (g > 4096) g = 4096;
+  const OutT *bias = (const OutT *)p.bias, *res = (const OutT *)p.res;
+  OutT *C = (OutT *)p.C;
+#define ZK_R(E) splitk_reduce<E, OutT><<<(unsigned)g, 256, 0, s>>>( \
+    ws, sp.splits, q.split_stride, p.M, p.N, bias, res, p.ldr, C, p.ldc)
+  switch (epi) {
+    case ZK_EPI_NONE: ZK_R(ZK_EPI_NONE); break;
+    case ZK_EPI_BIAS: ZK_R(ZK_EPI_BIAS); break;
+    case ZK_EPI_BIAS_GELU_ERF: ZK_R(ZK_EPI_BIAS_GELU_ERF); break;
+    case ZK_EPI_BIAS_GELU_TANH: ZK_R(ZK_EPI_BIAS_GELU_TANH); break;
+    case ZK_EPI_BIAS_RESIDUAL: ZK_R(ZK_EPI_BIAS_RESIDUAL); break;
+    case ZK_EPI_BIAS_RELU: ZK_R(ZK_EPI_BIAS_RELU); break;
+  }
+#undef ZK_R
 }
 
 // ------------------------------------------------------------- fp32 SIMT --
@@ -650,11 +748,10 @@ static int check_dims(const char *who, int64_t M, int64_t N, int64_t K) {
 
 using namespace zk;
 
-extern "C" int zk_gemm_f16(const void *A, const void *B, void *C, int64_t M,
-                           int64_t N, int64_t K, int64_t lda, int64_t ldb,
-                           int64_t ldc, int trans_b, int out_dtype,
-                           const void *bias, const void *residual, int64_t ldr,
-                           int epilogue, void *stream) {
+static int gemm_f16_impl(const void *A, const void *B, void *C, int64_t M, int64_t N,
+                         int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_b,
+                         int out_dtype, const void *bias, const void *residual, int64_t ldr,
+                         int epilogue, void *ws, int64_t ws_bytes, void *stream) {
   int st = check_dims("zk_gemm_f16", M, N, K);
   if (st) return st;
   if (M == 0 || N == 0) return ZK_OK;
@@ -679,9 +776,35 @@ extern "C" int zk_gemm_f16(const void *A, const void *B, void *C, int64_t M,
   if (K == 0) return fail(ZK_ERR_UNSUPPORTED, "zk_gemm_f16: K == 0");
   GemmParams p{A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc, bias, residual, ldr, 1.f, nullptr, 0};
   hipStream_t s = as_stream(stream);
-  if (out_dtype == ZK_F16) launch_mfma<F16Op, f16, false>(p, epilogue, s);
-  else launch_mfma<F16Op, float, false>(p, epilogue, s);
+  const SplitPlan sp = plan_split(M, N, K, 2);
+  if (ws && sp.splits > 1 && ws_bytes >= split_ws_bytes(M, N, sp) && aligned16(ws)) {
+    if (out_dtype == ZK_F16) launch_split<F16Op, f16>(p, epilogue, sp, (float *)ws, s);
+    else launch_split<F16Op, float>(p, epilogue, sp, (float *)ws, s);
+  } else if (out_dtype == ZK_F16) {
+    launch_mfma<F16Op, f16, false>(p, epilogue, s);
+  } else {
+    launch_mfma<F16Op, float, false>(p, epilogue, s);
+  }
   return check_launch("zk_gemm_f16");
+}
+
+extern "C" int zk_gemm_f16(const void *A, const void *B, void *C, int64_t M,
+                           int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                           int64_t ldc, int trans_b, int out_dtype,
+                           const void *bias, const void *residual, int64_t ldr,
+                           int epilogue, void *stream) {
+  return gemm_f16_impl(A, B, C, M, N, K, lda, ldb, ldc, trans_b, out_dtype, bias, residual, ldr,
+                       epilogue, nullptr, 0, stream);
+}
+
+extern "C" int zk_gemm_f16_ws(const void *A, const void *B, void *C, int64_t M, int64_t N,
+                              int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_b,
+                              int out_dtype, const void *bias, const void *residual,
+                              int64_t ldr, int epilogue, void *workspace, int64_t ws_bytes,
+                              void *stream) {
+  if (ws_bytes < 0) return fail(ZK_ERR_INVALID, "zk_gemm_f16_ws: negative workspace size");
+  return gemm_f16_impl(A, B, C, M, N, K, lda, ldb, ldc, trans_b, out_dtype, bias, residual, ldr,
+                       epilogue, workspace, ws_bytes, stream);
 }
 
 // Shape / operand checks shared by the int8 entry points.
@@ -751,9 +874,9 @@ extern "C" int zk_gemm_i8_requant(const int8_t *A, const int8_t *W, int8_t *Q, i
   return check_launch("zk_gemm_i8_requant");
 }
 
-extern "C" int zk_gemm_f32(const float *A, const float *B, float *C, int64_t M,
-                           int64_t N, int64_t K, int64_t lda, int64_t ldb,
-                           int64_t ldc, int trans_b, void *stream) {
+static int gemm_f32_impl(const float *A, const float *B, float *C, int64_t M, int64_t N,
+                         int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_b, void *ws,
+                         int64_t ws_bytes, void *stream) {
   int st = check_dims("zk_gemm_f32", M, N, K);
   if (st) return st;
   if (M == 0 || N == 0) return ZK_OK;
@@ -767,7 +890,11 @@ extern "C" int zk_gemm_f32(const float *A, const float *B, float *C, int64_t M,
   if (trans_b && K > 0 && K % 4 == 0 && lda % 4 == 0 && ldb % 4 == 0 && aligned16(A) &&
       aligned16(B) && lda < (1 << 21) && ldb < (1 << 21)) {
     GemmParams p{A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc, nullptr, nullptr, 0, 1.f, nullptr, 0};
-    launch_mfma<F32Op, float, false>(p, ZK_EPI_NONE, s);
+    const SplitPlan sp = plan_split(M, N, K, 4);
+    if (ws && sp.splits > 1 && ws_bytes >= split_ws_bytes(M, N, sp) && aligned16(ws))
+      launch_split<F32Op, float>(p, ZK_EPI_NONE, sp, (float *)ws, s);
+    else
+      launch_mfma<F32Op, float, false>(p, ZK_EPI_NONE, s);
     return check_launch("zk_gemm_f32");
   }
   if ((M + 63) / 64 > 65535) return fail(ZK_ERR_UNSUPPORTED, "zk_gemm_f32: M too large");
@@ -777,4 +904,24 @@ extern "C" int zk_gemm_f32(const float *A, const float *B, float *C, int64_t M,
   else
     gemm_f32_kernel<false><<<grid, 256, 0, s>>>(A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc);
   return check_launch("zk_gemm_f32");
+}
+
+extern "C" int zk_gemm_f32(const float *A, const float *B, float *C, int64_t M,
+                           int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                           int64_t ldc, int trans_b, void *stream) {
+  return gemm_f32_impl(A, B, C, M, N, K, lda, ldb, ldc, trans_b, nullptr, 0, stream);
+}
+
+extern "C" int zk_gemm_f32_ws(const float *A, const float *B, float *C, int64_t M, int64_t N,
+                              int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_b,
+                              void *workspace, int64_t ws_bytes, void *stream) {
+  if (ws_bytes < 0) return fail(ZK_ERR_INVALID, "zk_gemm_f32_ws: negative workspace size");
+  return gemm_f32_impl(A, B, C, M, N, K, lda, ldb, ldc, trans_b, workspace, ws_bytes, stream);
+}
+
+extern "C" int64_t zk_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int dtype) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  if (dtype == ZK_F16) return split_ws_bytes(M, N, plan_split(M, N, K, 2));
+  if (dtype == ZK_F32) return split_ws_bytes(M, N, plan_split(M, N, K, 4));
+  return 0;
 }

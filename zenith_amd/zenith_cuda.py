@@ -167,9 +167,22 @@ def _pad_k(t: torch.Tensor, mult: int) -> torch.Tensor:
     return out
 
 
+def gemm_workspace(M: int, N: int, K: int, dtype: int, device) -> torch.Tensor | None:
+    """Caller-side workspace for the split-K GEMMs (zk_gemm_workspace_size
+    bytes, from torch's caching allocator), or None when the product is not
+    split."""
+    n = int(L.load().zk_gemm_workspace_size(M, N, K, dtype))
+    return torch.empty(n, dtype=torch.uint8, device=device) if n > 0 else None
+
+
+def _ws_args(ws):
+    return (None, 0) if ws is None else (ws.data_ptr(), ws.numel())
+
+
 def _gemm_f16_nt(a: torch.Tensor, w: torch.Tensor, out_dtype, bias=None,
                  residual=None, epilogue=L.ZK_EPI_NONE) -> torch.Tensor:
-    """C[M,N] = epilogue(a[M,K] . w[N,K]^T) on the MFMA kernel."""
+    """C[M,N] = epilogue(a[M,K] . w[N,K]^T) on the MFMA kernel (split along K
+    with a workspace when M is small)."""
     M, K = a.shape
     N = w.shape[0]
     a = _pad_k(a, 8)
@@ -179,9 +192,10 @@ def _gemm_f16_nt(a: torch.Tensor, w: torch.Tensor, out_dtype, bias=None,
     if residual is not None:
         residual = residual.contiguous()
         ldr = residual.stride(0)
-    L.call("zk_gemm_f16", _p(a), _p(w), _p(out), M, N, a.shape[1], a.stride(0),
+    ws = gemm_workspace(M, N, a.shape[1], L.ZK_F16, a.device) if M else None
+    L.call("zk_gemm_f16_ws", _p(a), _p(w), _p(out), M, N, a.shape[1], a.stride(0),
            w.stride(0), out.stride(0), 1, _DT[out_dtype], _p(bias), _p(residual), ldr,
-           epilogue, _stream(a))
+           epilogue, *_ws_args(ws), _stream(a))
     return out
 
 
@@ -306,7 +320,9 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
     M = x2.shape[0]
     y = torch.empty((M, N), dtype=torch.float32, device=x.device)
     if M:
-        L.call("zk_gemm_f32", _p(x2), _p(w), _p(y), M, N, K, K, K, N, 1, _stream(x2))
+        ws = gemm_workspace(M, N, K, L.ZK_F32, x.device)
+        L.call("zk_gemm_f32_ws", _p(x2), _p(w), _p(y), M, N, K, K, K, N, 1, *_ws_args(ws),
+               _stream(x2))
     if bias is not None:
         if activation in ("gelu", "gelu_erf", "gelu_tanh"):
             y = bias_gelu(y, bias.contiguous(),
