@@ -225,6 +225,30 @@ int zk_gemm_f32_ws(const float *A, const float *B, float *C, int64_t M, int64_t 
                    int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_b,
                    void *workspace, int64_t ws_bytes, void *stream);
 
+/* Embedding gather, out[i, :] = table[ids[i], :] for int32 ids [n] and a
+ * [vocab, hidden] table in dtype ZK_F32 or ZK_F16; an id outside [0, vocab)
+ * gives a zero row. Replaces embedding_f32
+ * (core/src/transformer_kernels.cu:236-262). */
+int zk_embedding(const int32_t *ids, const void *table, void *out, int64_t n,
+                 int64_t hidden, int64_t vocab, int dtype, void *stream);
+
+/* BERT input layer in one pass per token:
+ *   out[b, s, :] = LayerNorm(word[ids[b,s]] + pos[s + pos_offset]
+ *                            + type[token_type_ids[b,s]]) * gamma + beta
+ * ids / token_type_ids int32 [batch, seq] (token_type_ids may be NULL: type
+ * 0); tables [vocab | max_pos | n_types, hidden] and gamma / beta [hidden] in
+ * dtype ZK_F32 or ZK_F16; fp32 two-pass statistics; hidden a multiple of the
+ * 16-byte vector and at most 4096 (fp16) / 2048 (fp32). An id outside its
+ * table contributes nothing. The composition of the reference's embedding
+ * gather (transformer_kernels.cu:236-262) with the HF BertEmbeddings sum and
+ * LayerNorm that its loaders target (benchmarks/bert_fp16_full.py:45-94). */
+int zk_bert_embeddings(const int32_t *input_ids, const int32_t *token_type_ids,
+                       const void *word, const void *pos, const void *type_table,
+                       const void *gamma, const void *beta, void *out, int64_t batch,
+                       int64_t seq, int64_t hidden, int64_t vocab, int64_t max_pos,
+                       int64_t n_types, int64_t pos_offset, float eps, int dtype,
+                       void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,99 @@
+"""GPU parity: embedding gather, the fused BERT embedding layer, and the full
+BertModel (embeddings + fp16 encoder) loaded from a transformers model and
+from a saved checkpoint, vs the CPU oracle and transformers' own forward."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ops
+from tests.conftest import fp16_tol
+from zenith_amd import synthetic
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype,H", [(torch.float32, 768), (torch.float16, 768), (torch.float32, 30)])
+def test_embedding_gather(dev, dtype, H):
+    from zenith_amd import _lib as L
+
+    V, n = 1000, 777
+    table = torch.from_numpy(synthetic.normal((V, H), tag=1)).to(dev, dtype)
+    ids = torch.from_numpy(np.random.default_rng(1).integers(-5, V + 5, n).astype(np.int32)).to(dev)
+    out = torch.empty((n, H), dtype=dtype, device=dev)
+    L.call("zk_embedding", ids.data_ptr(), table.data_ptr(), out.data_ptr(), n, H, V,
+           L.ZK_F32 if dtype == torch.float32 else L.ZK_F16, torch.cuda.current_stream().cuda_stream)
+    idn = ids.cpu().numpy()
+    ok = (idn >= 0) & (idn < V)
+    ref = np.zeros((n, H), np.float32)
+    ref[ok] = table.float().cpu().numpy()[idn[ok]]
+    np.testing.assert_array_equal(out.float().cpu().numpy(), ref)
+
+
+def _hf_model(layers=2, act="gelu", seed=0):
+    transformers = pytest.importorskip("transformers")
+    torch.manual_seed(seed)
+    cfg = transformers.BertConfig(hidden_size=768, num_attention_heads=12, intermediate_size=3072,
+                                  num_hidden_layers=layers, hidden_act=act, vocab_size=5000,
+                                  max_position_embeddings=512, type_vocab_size=2)
+    cfg._attn_implementation = "eager"
+    return transformers.BertModel(cfg, add_pooling_layer=False).eval()
+
+
+def test_bert_embeddings_vs_oracle(dev):
+    from zenith_amd.bert_model import BertModel
+
+    hf = _hf_model(layers=1)
+    m = BertModel.from_hf(hf, device=dev)
+    B, S = 3, 100
+    rng = np.random.default_rng(2)
+    ids = rng.integers(0, 5000, (B, S)).astype(np.int32)
+    tt = rng.integers(0, 2, (B, S)).astype(np.int32)
+    y = m.embed(torch.from_numpy(ids), torch.from_numpy(tt), pos_offset=7).float().cpu().numpy()
+    sd = {k: v.detach().numpy() for k, v in hf.state_dict().items()}
+    r16 = synthetic.round_f16
+    x = (r16(sd["embeddings.word_embeddings.weight"])[ids]
+         + r16(sd["embeddings.position_embeddings.weight"])[7:7 + S][None]
+         + r16(sd["embeddings.token_type_embeddings.weight"])[tt])
+    ref = ops.layernorm(x.reshape(B * S, 768), r16(sd["embeddings.LayerNorm.weight"]),
+                        r16(sd["embeddings.LayerNorm.bias"]), 1e-12).reshape(B, S, 768)
+    ok, worst = fp16_tol(y, ref)
+    assert ok, worst
+
+
+@pytest.mark.parametrize("act", ["gelu", "gelu_new"])
+def test_bert_model_vs_transformers(dev, act, tmp_path):
+    """Full model from input_ids with right padding, against transformers'
+    fp32 forward; then the same weights through save_pretrained (safetensors)
+    and from_pretrained give bit-identical outputs."""
+    from zenith_amd.bert_model import BertModel
+
+    hf = _hf_model(layers=2, act=act, seed=1)
+    B, S = 4, 128
+    rng = np.random.default_rng(3)
+    ids = rng.integers(0, 5000, (B, S)).astype(np.int64)
+    tt = rng.integers(0, 2, (B, S)).astype(np.int64)
+    lens = synthetic.padding_lengths(B, S, seed=3)
+    mask = (np.arange(S)[None, :] < lens[:, None]).astype(np.int64)
+    with torch.no_grad():
+        ref = hf(input_ids=torch.from_numpy(ids), attention_mask=torch.from_numpy(mask),
+                 token_type_ids=torch.from_numpy(tt)).last_hidden_state.numpy()
+    m = BertModel.from_hf(hf, device=dev)
+    y = m(torch.from_numpy(ids), attention_mask=torch.from_numpy(mask),
+          token_type_ids=torch.from_numpy(tt)).float().cpu().numpy()
+    rel = np.linalg.norm(y - ref) / np.linalg.norm(ref)
+    assert rel < 2e-2 and np.all(np.abs(y - ref) <= 2e-2 + 2e-2 * np.abs(ref)), rel
+    hf.save_pretrained(tmp_path, safe_serialization=True)
+    m2 = BertModel.from_pretrained(str(tmp_path), device=dev)
+    y2 = m2(torch.from_numpy(ids), attention_mask=torch.from_numpy(mask),
+            token_type_ids=torch.from_numpy(tt)).float().cpu().numpy()
+    np.testing.assert_array_equal(y2, y)
+
+
+def test_bert_model_rejects_non_prefix_mask(dev):
+    from zenith_amd.bert_model import BertModel
+
+    m = BertModel.from_hf(_hf_model(layers=1), device=dev)
+    ids = torch.zeros((1, 8), dtype=torch.int32)
+    with pytest.raises(RuntimeError):
+        m(ids, attention_mask=torch.tensor([[1, 0, 1, 1, 1, 1, 1, 1]]))
