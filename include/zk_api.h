@@ -59,6 +59,18 @@ int zk_version(void);
  * relu_f32 core/src/cuda_kernels.cu:504-507. */
 int zk_relu(const void *x, void *y, int64_t n, int dtype, void *stream);
 
+/* y = 1 / (1 + exp(-x)), n elements, dtype ZK_F32 or ZK_F16. x may equal y.
+ * The kernel behind the ONNX Sigmoid operator's GPU branch
+ * (zenith/execution/operators/activation_ops.py:82-91, which calls
+ * _zenith_core.cuda.sigmoid_gpu; the reference binds no such function, so
+ * its branch always falls back to NumPy). */
+int zk_sigmoid(const void *x, void *y, int64_t n, int dtype, void *stream);
+
+/* y = tanh(x), n elements, dtype ZK_F32 or ZK_F16. x may equal y. The
+ * kernel behind the ONNX Tanh operator's GPU branch (activation_ops.py:111-120,
+ * cuda.tanh_gpu, likewise unbound in the reference) and the BERT pooler. */
+int zk_tanh(const void *x, void *y, int64_t n, int dtype, void *stream);
+
 /* y[r, c] = GELU(x[r, c] + bias[c]); bias may be NULL. rows*cols elements,
  * contiguous. dtype ZK_F32 or ZK_F16 (fp32 math either way).
  * Replaces zenith_cuda.gelu (cuda_bindings.cpp:48-56 -> cuda_kernels.cu:

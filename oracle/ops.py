@@ -47,6 +47,19 @@ def relu(x: np.ndarray) -> np.ndarray:
     return np.maximum(x, 0).astype(x.dtype, copy=False)
 
 
+def sigmoid(x: np.ndarray) -> np.ndarray:
+    """1 / (1 + exp(-x)) in float32 (execute_sigmoid,
+    zenith/execution/operators/activation_ops.py:76-93)."""
+    x = x.astype(F32, copy=False)
+    with np.errstate(over="ignore"):
+        return (F32(1.0) / (F32(1.0) + np.exp(-x))).astype(F32, copy=False)
+
+
+def tanh(x: np.ndarray) -> np.ndarray:
+    """tanh(x) in float32 (execute_tanh, activation_ops.py:105-122)."""
+    return np.tanh(x.astype(F32, copy=False))
+
+
 def gelu_tanh(x: np.ndarray) -> np.ndarray:
     """0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) evaluated in float32
     (gelu_kernel core/src/cuda_kernels.cu:115-126; fused_bias_gelu_cpu

@@ -24,6 +24,7 @@ def test_invalid_gpu_tensor():
     (cuda.add_2d_gpu, 2), (cuda.fused_add_layernorm_gpu, 4), (cuda.fused_bias_gelu_gpu, 2),
     (cuda.attention_fp16_gpu, 3), (cuda.attention_full_fp16_gpu, 3), (cuda.linear_fp16_gpu, 3),
     (cuda.gelu_fp16_gpu, 1), (cuda.layernorm_fp16_gpu, 3), (cuda.add_fp16_gpu, 2),
+    (cuda.relu_gpu, 1), (cuda.sigmoid_gpu, 1), (cuda.tanh_gpu, 1), (cuda.add_gpu, 2),
 ])
 def test_invalid_inputs_raise(fn, args):
     with pytest.raises(RuntimeError):
@@ -44,3 +45,30 @@ def test_gpu_tensor_rejects_cpu_data():
 
     with pytest.raises(RuntimeError):
         cuda.GpuTensor(torch.zeros(3))
+
+
+def test_onnx_branch_surface():
+    """Every function the ONNX operators' GPU branches and ExecutionContext
+    call on ``_zenith_core.cuda`` (activation_ops.py:52-181,
+    math_ops.py:83-190, context.py:56-182) exists with the reference's name."""
+    for name in ("is_available", "to_gpu", "to_numpy", "relu_gpu", "sigmoid_gpu", "tanh_gpu",
+                 "softmax_gpu", "gelu_gpu", "matmul", "add"):
+        assert callable(getattr(cuda, name)), name
+    with pytest.raises(RuntimeError):
+        cuda.to_numpy(cuda.GpuTensor())
+    with pytest.raises(RuntimeError):
+        cuda.to_numpy([1.0])
+
+
+def test_no_gpu_reports_unavailable():
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    assert cuda.is_available() is False
+    assert set(cuda.memory_stats()) == {"allocations", "cache_hits", "cache_returns",
+                                        "total_allocated"}
+    for fn, args in ((cuda.matmul, ([[1.0]], [[1.0]])), (cuda.add, ([1.0], [1.0])),
+                     (cuda.relu, ([1.0],)), (cuda.softmax, ([[1.0]],))):
+        with pytest.raises(RuntimeError):
+            fn(*args)

@@ -30,14 +30,14 @@ def test_embedding_gather(dev, dtype, H):
     np.testing.assert_array_equal(out.float().cpu().numpy(), ref)
 
 
-def _hf_model(layers=2, act="gelu", seed=0):
+def _hf_model(layers=2, act="gelu", seed=0, pooler=False):
     transformers = pytest.importorskip("transformers")
     torch.manual_seed(seed)
     cfg = transformers.BertConfig(hidden_size=768, num_attention_heads=12, intermediate_size=3072,
                                   num_hidden_layers=layers, hidden_act=act, vocab_size=5000,
                                   max_position_embeddings=512, type_vocab_size=2)
     cfg._attn_implementation = "eager"
-    return transformers.BertModel(cfg, add_pooling_layer=False).eval()
+    return transformers.BertModel(cfg, add_pooling_layer=pooler).eval()
 
 
 def test_bert_embeddings_vs_oracle(dev):
@@ -97,3 +97,36 @@ def test_bert_model_rejects_non_prefix_mask(dev):
     ids = torch.zeros((1, 8), dtype=torch.int32)
     with pytest.raises(RuntimeError):
         m(ids, attention_mask=torch.tensor([[1, 0, 1, 1, 1, 1, 1, 1]]))
+
+
+def test_bert_pooler_vs_transformers(dev, tmp_path):
+    """pooler_output = tanh(dense(h[:, 0])) against transformers' BertPooler
+    on the same model, and through a saved checkpoint; a model without
+    pooler weights refuses `pool`."""
+    from zenith_amd.bert_model import BertModel
+
+    hf = _hf_model(layers=1, act="gelu", seed=4, pooler=True)
+    B, S = 5, 64
+    rng = np.random.default_rng(5)
+    ids = rng.integers(0, 5000, (B, S)).astype(np.int64)
+    with torch.no_grad():
+        out = hf(input_ids=torch.from_numpy(ids))
+    m = BertModel.from_hf(hf, device=dev)
+    h = m(torch.from_numpy(ids))
+    p = m.pool(h).float().cpu().numpy()
+    ref = out.pooler_output.numpy()
+    assert p.shape == (B, 768)
+    assert np.all(np.abs(p - ref) <= 2e-2 + 2e-2 * np.abs(ref)), np.abs(p - ref).max()
+    # the pooler alone, on the model's own hidden state, vs the oracle
+    sd = {k: v.detach().numpy() for k, v in hf.state_dict().items()}
+    cls = h[:, 0].float().cpu().numpy()
+    r16 = synthetic.round_f16
+    ref2 = ops.tanh(ops.matmul_f64(cls, r16(sd["pooler.dense.weight"]).T).astype(np.float32)
+                    + r16(sd["pooler.dense.bias"]))
+    ok, worst = fp16_tol(p, ref2)
+    assert ok, worst
+    hf.save_pretrained(tmp_path, safe_serialization=True)
+    m2 = BertModel.from_pretrained(str(tmp_path), device=dev)
+    np.testing.assert_array_equal(m2.pool(m2(torch.from_numpy(ids))).float().cpu().numpy(), p)
+    with pytest.raises(RuntimeError):
+        BertModel.from_hf(_hf_model(layers=1), device=dev).pool(h)

@@ -81,6 +81,71 @@ def test_matmul_linear(dev):
         cuda.matmul_gpu(A, A)
 
 
+@pytest.mark.parametrize("M,K,N", [(128, 256, 384), (1, 768, 3072), (300, 64, 200), (33, 12, 5)])
+def test_matmul_paths(dev, M, K, N):
+    """matmul_gpu / NumPy matmul: products with K % 4 == 0 and at least 2^18
+    multiply-adds transpose B and run on the fp32 MFMA GEMM, the rest on the
+    SIMT kernel; both against the float64-accumulated product."""
+    cuda = _c()
+    a = synthetic.normal((M, K), tag=30)
+    b = synthetic.normal((K, N), tag=31)
+    ref = ops.matmul_f64(a, b)
+    np.testing.assert_allclose(cuda.matmul_gpu(cuda.to_gpu(a), cuda.to_gpu(b)).to_numpy(), ref,
+                               rtol=1e-4, atol=1e-4)
+    y = cuda.matmul(a, b)
+    assert isinstance(y, np.ndarray) and y.dtype == np.float32 and y.shape == (M, N)
+    np.testing.assert_allclose(y, ref, rtol=1e-4, atol=1e-4)
+    with pytest.raises(RuntimeError):
+        cuda.matmul(a, a.T[:-1])
+
+
+def test_onnx_branch_functions(dev):
+    """What the ONNX operators' GPU branches call, in their order
+    (activation_ops.py:52-181: upload with to_gpu, the *_gpu function, the
+    module-level to_numpy; math_ops.py:83-190: NumPy matmul and 4D add), vs
+    the operators' own NumPy formulas (the oracle)."""
+    cuda = _c()
+    assert cuda.is_available()
+    x = synthetic.normal((2, 3, 5, 7), tag=32) * 3
+    X = cuda.to_gpu(x)
+    for name, ref, rtol in (("relu_gpu", ops.relu(x), 0), ("sigmoid_gpu", ops.sigmoid(x), 2e-6),
+                            ("tanh_gpu", ops.tanh(x), 2e-6), ("gelu_gpu", ops.gelu_tanh(x), 1e-5)):
+        y = cuda.to_numpy(getattr(cuda, name)(X))
+        assert y.shape == x.shape and y.dtype == np.float32, name
+        np.testing.assert_allclose(y, ref, rtol=rtol, atol=1e-6, err_msg=name)
+    x2 = x.reshape(6, 35)
+    np.testing.assert_allclose(cuda.to_numpy(cuda.softmax_gpu(cuda.to_gpu(x2))), ops.softmax(x2),
+                               rtol=1e-5, atol=1e-7)
+    with pytest.raises(RuntimeError):  # 2D only, as in the reference
+        cuda.softmax_gpu(X)
+    z = synthetic.normal(x.shape, tag=33)
+    np.testing.assert_array_equal(cuda.add(x, z), x + z)
+    np.testing.assert_array_equal(cuda.add_gpu(X, cuda.to_gpu(z)).to_numpy(), x + z)
+    with pytest.raises(RuntimeError):
+        cuda.add(x, z[:1])
+
+
+def test_numpy_interface(dev):
+    """NumPy-array functions (bindings.cpp:2010-2131 and the cuDNN-backed
+    relu / add) vs the oracle."""
+    cuda = _c()
+    x = synthetic.normal((17, 768), tag=34) * 2
+    g = 1 + synthetic.normal((768,), tag=35, std=0.1)
+    b = synthetic.normal((768,), tag=36, std=0.1)
+    np.testing.assert_array_equal(cuda.relu(x), ops.relu(x))
+    np.testing.assert_allclose(cuda.gelu(x), ops.gelu_tanh(x), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(cuda.layernorm(x, g, b), ops.layernorm(x, g, b, 1e-5),
+                               rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(cuda.layernorm(x, g, b, 1e-12), ops.layernorm(x, g, b, 1e-12),
+                               rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(cuda.softmax(x), ops.softmax(x), rtol=1e-5, atol=1e-7)
+    for fn, args in ((cuda.gelu, (x[0],)), (cuda.softmax, (x[0],)), (cuda.layernorm, (x[0], g, b))):
+        with pytest.raises(RuntimeError):
+            fn(*args)
+    st = cuda.memory_stats()
+    assert st["total_allocated"] > 0 and st["allocations"] > 0
+
+
 def test_layout_ops(dev):
     cuda = _c()
     B, S, H, D = 2, 5, 3, 8

@@ -106,6 +106,42 @@ def test_relu(dev, n, dtype):
     np.testing.assert_array_equal(y, ops.relu(x.astype(np.float16 if dtype == torch.float16 else np.float32)).astype(np.float32))
 
 
+@pytest.mark.parametrize("op", ["sigmoid", "tanh"])
+@pytest.mark.parametrize("n", [1, 9, 4096 * 768 + 3])
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_sigmoid_tanh(dev, op, n, dtype, offset):
+    """zk_sigmoid / zk_tanh through the C ABI: the vector body, the scalar
+    tail, a misaligned start (offset 1 takes the scalar kernel), saturation
+    at +-inf and large |x|, NaN propagation. fp32: a few ulp of the float32
+    oracle; fp16: the fp16 bar on fp16-rounded inputs."""
+    from zenith_amd import _lib as L
+
+    x = synthetic.normal((n + offset,), tag=17) * 4
+    x[offset: offset + 6] = np.array([0.0, -np.inf, np.inf, 100.0, -100.0, np.nan],
+                                     np.float32)[: min(n, 6)]
+    tdt = torch.float32 if dtype == "f32" else torch.float16
+    if dtype == "f16":
+        x = synthetic.round_f16(x)
+    xt = _t(x, dev, tdt)[offset:]
+    y = torch.empty_like(xt)
+    L.call("zk_" + op, xt.data_ptr(), y.data_ptr(), n,
+           L.ZK_F32 if dtype == "f32" else L.ZK_F16, torch.cuda.current_stream().cuda_stream)
+    ref = getattr(ops, op)(x[offset:])
+    y = y.float().cpu().numpy()
+    assert np.array_equal(np.isnan(y), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    if dtype == "f32":
+        np.testing.assert_allclose(y[ok], ref[ok], rtol=2e-6, atol=1e-7)
+    else:
+        good, worst = fp16_tol(y[ok], ref[ok])
+        assert good, worst
+    if n >= 6 and offset == 0:
+        sat = y[1:5]
+        expect = [0.0, 1.0, 1.0, 0.0] if op == "sigmoid" else [-1.0, 1.0, 1.0, -1.0]
+        assert sat.tolist() == expect and y[0] == (0.5 if op == "sigmoid" else 0.0)
+
+
 @pytest.mark.parametrize("n", [1, 9, 4096 * 768, 4096 * 3072 + 3])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 def test_quantize_bit_exact(dev, n, dtype):

@@ -104,6 +104,22 @@ def test_add_layernorm_vs_reference_build():
 
 
 # ------------------------------------------------------------------ GELU ---
+def test_sigmoid_tanh_closed_forms():
+    """sigmoid(0) = 1/2, sigmoid(x) + sigmoid(-x) = 1, saturation at +-inf,
+    tanh(x) = 2 sigmoid(2x) - 1, and both vs torch's library routines."""
+    import torch
+
+    assert ops.sigmoid(np.zeros(3, np.float32)).tolist() == [0.5] * 3
+    assert ops.sigmoid(np.array([-np.inf, np.inf], np.float32)).tolist() == [0.0, 1.0]
+    x = np.linspace(-12, 12, 2001, dtype=np.float32)
+    np.testing.assert_allclose(ops.sigmoid(x) + ops.sigmoid(-x), 1.0, atol=1e-6)
+    np.testing.assert_allclose(ops.tanh(x), 2 * ops.sigmoid(2 * x) - 1, atol=2e-6)
+    np.testing.assert_allclose(ops.tanh(-x), -ops.tanh(x), atol=0)
+    t = torch.from_numpy(x)
+    np.testing.assert_allclose(ops.sigmoid(x), torch.sigmoid(t).numpy(), rtol=2e-7, atol=1e-7)
+    np.testing.assert_allclose(ops.tanh(x), torch.tanh(t).numpy(), rtol=2e-7, atol=1e-7)
+
+
 def test_gelu_reference_kats():
     for fn in (ops.gelu_tanh, ops.gelu_erf):
         y = fn(np.array([1.0, 0.0, -1.0], np.float32))

@@ -39,6 +39,8 @@ SIGNATURES: dict[str, list] = {
     "zk_last_error": [],
     "zk_version": [],
     "zk_relu": [_vp, _vp, _i64, _i32, _vp],
+    "zk_sigmoid": [_vp, _vp, _i64, _i32, _vp],
+    "zk_tanh": [_vp, _vp, _i64, _i32, _vp],
     "zk_gelu": [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp],
     "zk_layernorm": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp],
     "zk_layernorm_q8": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _f32, _vp],

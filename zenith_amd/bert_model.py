@@ -10,8 +10,10 @@ stores Linear weights as W[out, in], which is the layout the encoder keeps
 bert_hybrid.py:45-94, read the same tensors). hidden_act "gelu" selects the
 erf GELU epilogue and "gelu_new" / "gelu_pytorch_tanh" the tanh one.
 
-Not provided: the pooler head (dense + tanh over [CLS]); `forward` returns
-last_hidden_state.
+`forward` returns last_hidden_state; `pool` is the pooler head,
+tanh(dense(h[:, 0])) over the [CLS] rows (the reference's BERT benchmark
+model, benchmarks/bert_benchmark.py:101-107, and transformers' BertPooler),
+present when the checkpoint holds pooler weights.
 """
 
 from __future__ import annotations
@@ -24,6 +26,7 @@ import torch
 
 from . import _lib as L
 from .encoder import BertEncoder
+from .zenith_cuda import _ws_args, gemm_workspace
 
 F16 = torch.float16
 
@@ -43,6 +46,7 @@ _EMB_KEYS = {
     "type": "embeddings.token_type_embeddings.weight",
     "ln_g": "embeddings.LayerNorm.weight", "ln_b": "embeddings.LayerNorm.bias",
 }
+_POOLER_KEYS = {"W": "pooler.dense.weight", "b": "pooler.dense.bias"}
 _GELU = {"gelu": "erf", "gelu_new": "tanh", "gelu_pytorch_tanh": "tanh", "gelu_fast": "tanh"}
 
 
@@ -55,7 +59,7 @@ def _np32(t) -> np.ndarray:
 def split_state_dict(sd: dict, num_layers: int) -> tuple[dict, list[dict]]:
     """HF BERT state dict (with or without a leading "bert.") -> (embedding
     tables, per-layer weight dicts in the encoder's key names)."""
-    prefix = "bert." if any(k.startswith("bert.") for k in sd) else ""
+    prefix = _prefix(sd)
     get = lambda k: _np32(sd[prefix + k])  # noqa: E731
     emb = {n: get(k) for n, k in _EMB_KEYS.items()}
     layers = [{n: get(f"encoder.layer.{i}.{k}") for n, k in _LAYER_KEYS.items()}
@@ -63,11 +67,25 @@ def split_state_dict(sd: dict, num_layers: int) -> tuple[dict, list[dict]]:
     return emb, layers
 
 
+def pooler_weights(sd: dict) -> dict | None:
+    """{"W": [H, H], "b": [H]} of the pooler dense layer, or None when the
+    state dict has none (add_pooling_layer=False, masked-LM heads)."""
+    prefix = _prefix(sd)
+    if prefix + _POOLER_KEYS["W"] not in sd:
+        return None
+    return {n: _np32(sd[prefix + k]) for n, k in _POOLER_KEYS.items()}
+
+
+def _prefix(sd: dict) -> str:
+    return "bert." if any(k.startswith("bert.") for k in sd) else ""
+
+
 class BertModel:
     """Embeddings + encoder; input_ids [B, S] -> last_hidden_state [B, S, H] fp16."""
 
     def __init__(self, emb: dict, layers: list[dict], heads: int = 12, eps: float = 1e-12,
-                 gelu: str = "erf", device: str | torch.device = "cuda"):
+                 gelu: str = "erf", device: str | torch.device = "cuda",
+                 pooler: dict | None = None):
         self.device = torch.device(device)
         L.load()
         self.eps = float(eps)
@@ -76,6 +94,11 @@ class BertModel:
         self.word, self.pos, self.type = to(emb["word"]), to(emb["pos"]), to(emb["type"])
         self.ln_g, self.ln_b = to(emb["ln_g"]), to(emb["ln_b"])
         self.hidden = self.word.shape[1]
+        self.pool_w = self.pool_b = None
+        if pooler is not None:
+            self.pool_w, self.pool_b = to(pooler["W"]), to(pooler["b"])
+            if self.pool_w.shape != (self.hidden, self.hidden) or self.pool_b.shape != (self.hidden,):
+                raise RuntimeError("pooler weights must be [hidden, hidden] and [hidden]")
 
     # ----------------------------------------------------------- loaders --
     @classmethod
@@ -83,9 +106,11 @@ class BertModel:
         """From a transformers BertModel (or a model with a `.bert` member)."""
         bert = getattr(model, "bert", model)
         cfg = bert.config
-        emb, layers = split_state_dict(bert.state_dict(), cfg.num_hidden_layers)
+        sd = bert.state_dict()
+        emb, layers = split_state_dict(sd, cfg.num_hidden_layers)
         return cls(emb, layers, heads=cfg.num_attention_heads, eps=cfg.layer_norm_eps,
-                   gelu=_GELU.get(cfg.hidden_act, "erf"), device=device)
+                   gelu=_GELU.get(cfg.hidden_act, "erf"), device=device,
+                   pooler=pooler_weights(sd))
 
     @classmethod
     def from_pretrained(cls, path: str, device: str | torch.device = "cuda") -> "BertModel":
@@ -104,7 +129,8 @@ class BertModel:
         emb, layers = split_state_dict(sd, int(cfg["num_hidden_layers"]))
         return cls(emb, layers, heads=int(cfg["num_attention_heads"]),
                    eps=float(cfg.get("layer_norm_eps", 1e-12)),
-                   gelu=_GELU.get(cfg.get("hidden_act", "gelu"), "erf"), device=device)
+                   gelu=_GELU.get(cfg.get("hidden_act", "gelu"), "erf"), device=device,
+                   pooler=pooler_weights(sd))
 
     # ----------------------------------------------------------- forward --
     def embed(self, input_ids: torch.Tensor, token_type_ids: torch.Tensor | None = None,
@@ -135,6 +161,27 @@ class BertModel:
         return self.encoder(x, lengths)
 
     __call__ = forward
+
+    def pool(self, hidden: torch.Tensor) -> torch.Tensor:
+        """pooler_output [B, H] fp16 = tanh(hidden[:, 0] @ W^T + b). The
+        GEMM reads the [CLS] rows in place (leading dimension S*H) with the
+        bias in its epilogue; tanh runs in place on the [B, H] result."""
+        if self.pool_w is None:
+            raise RuntimeError("this model has no pooler weights")
+        if (hidden.dim() != 3 or hidden.shape[2] != self.hidden or hidden.dtype != F16
+                or not hidden.is_contiguous() or hidden.device.type != "cuda"):
+            raise RuntimeError("pool expects the contiguous fp16 [B, S, hidden] encoder output")
+        B, S, H = hidden.shape
+        out = torch.empty((B, H), dtype=F16, device=self.device)
+        if B == 0:
+            return out
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        ws = gemm_workspace(B, H, H, L.ZK_F16, self.device)
+        L.call("zk_gemm_f16_ws", hidden.data_ptr(), self.pool_w.data_ptr(), out.data_ptr(),
+               B, H, H, S * H, H, H, 1, L.ZK_F16, self.pool_b.data_ptr(), None, 0, L.ZK_EPI_BIAS,
+               *_ws_args(ws), stream)
+        L.call("zk_tanh", out.data_ptr(), out.data_ptr(), B * H, L.ZK_F16, stream)
+        return out
 
     def _ids(self, t) -> torch.Tensor:
         t = torch.as_tensor(t)

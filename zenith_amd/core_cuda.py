@@ -8,6 +8,17 @@ outputs, and RuntimeError on the same preconditions. It is the API behind the
 reference's published BERT comparator (benchmarks/bert_hybrid.py:96-146);
 a caller switches with ``from zenith_amd import core_cuda as cuda``.
 
+It also carries what the GPU branches of the reference's ONNX operators call
+(zenith/execution/operators/activation_ops.py:52-181, math_ops.py:83-190,
+context.py:56-182): is_available, to_gpu, to_numpy, relu_gpu, sigmoid_gpu,
+tanh_gpu, softmax_gpu, gelu_gpu and the NumPy-array functions matmul and add,
+so those branches reach the HIP kernels when this module stands in for
+``_zenith_core.cuda``. (In the reference, to_numpy is only a GpuTensor method
+and sigmoid_gpu / tanh_gpu are not bound, so those branches always end in the
+operators' NumPy fallbacks.) The NumPy-array functions gelu, layernorm and
+softmax (bindings.cpp:2010-2131) are here too; the cuDNN convolution, pooling
+and batch-norm functions are not (no CNN path in this build).
+
 Differences from the reference, by design:
   - every operation runs a kernel of libzenith_hip.so on torch's current
     stream (no cuBLAS; the `*_fp16_gpu` functions convert with zk_convert,
@@ -110,6 +121,50 @@ def sync() -> None:
     torch.cuda.synchronize()
 
 
+def is_available() -> bool:
+    """True when a GPU is visible and the HIP kernel library loads
+    (bindings.cpp:684-686)."""
+    if not torch.cuda.is_available():
+        return False
+    try:
+        L.load()
+    except RuntimeError:
+        return False
+    return True
+
+
+def memory_stats() -> dict:
+    """Device-memory pool statistics under the reference's keys
+    (bindings.cpp:825-836, pool of core/include/zenith/gpu_tensor.hpp:26-95),
+    read from torch's caching allocator, which plays that pool's part here:
+    allocations = device allocations made (pool misses), cache_hits =
+    requests served from the cache, cache_returns = blocks given back to the
+    cache, total_allocated = bytes ever obtained from the device."""
+    st = torch.cuda.memory_stats() if torch.cuda.is_available() else {}
+    requests = int(st.get("allocation.all.allocated", 0))
+    segments = int(st.get("segment.all.allocated", 0))
+    return {
+        "allocations": segments,
+        "cache_hits": max(requests - segments, 0),
+        "cache_returns": int(st.get("allocation.all.freed", 0)),
+        "total_allocated": int(st.get("reserved_bytes.all.allocated", 0)),
+    }
+
+
+def clear_memory_pool() -> None:
+    """Return cached, unused device memory (bindings.cpp:838-839)."""
+    if torch.cuda.is_available():
+        torch.cuda.empty_cache()
+
+
+def to_numpy(tensor: GpuTensor) -> np.ndarray:
+    """Copy a GpuTensor to a new NumPy array; the module-level form the
+    ONNX operators' GPU branches call (activation_ops.py:59,88,117,148,181)."""
+    if not isinstance(tensor, GpuTensor):
+        raise RuntimeError("to_numpy requires a GpuTensor")
+    return tensor.to_numpy()
+
+
 # --------------------------------------------------------------- helpers ---
 def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
@@ -193,12 +248,29 @@ def matmul_gpu(A: GpuTensor, B: GpuTensor) -> GpuTensor:
         raise RuntimeError("matmul_gpu requires 2D tensors")
     if A.dim(1) != B.dim(0):
         raise RuntimeError("matmul_gpu dimension mismatch")
-    a, b = A.tensor, B.tensor
+    return GpuTensor(_matmul_nn(A.tensor, B.tensor))
+
+
+# Products of at least this many multiply-adds transpose B once and run on
+# the fp32 MFMA GEMM (which reads B as [N, K]); smaller ones, and K not a
+# multiple of 4, take the SIMT kernel in one launch.
+_MFMA_MIN_MACS = 1 << 18
+
+
+def _matmul_nn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     M, K = a.shape
     N = b.shape[1]
     c = _new(a, (M, N))
-    L.call("zk_gemm_f32", a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K, K, N, N, 0, _stream(a))
-    return GpuTensor(c)
+    s = _stream(a)
+    if K % 4 == 0 and M * N * K >= _MFMA_MIN_MACS:
+        bt = _new(b, (N, K))
+        L.call("zk_transpose_0213", b.data_ptr(), bt.data_ptr(), 1, K, N, 1, L.ZK_F32, s)
+        ws = gemm_workspace(M, N, K, L.ZK_F32, a.device)
+        L.call("zk_gemm_f32_ws", a.data_ptr(), bt.data_ptr(), c.data_ptr(), M, N, K, K, K, N, 1,
+               *_ws_args(ws), s)
+    else:
+        L.call("zk_gemm_f32", a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K, K, N, N, 0, s)
+    return c
 
 
 def linear_gpu(X: GpuTensor, W: GpuTensor, bias: GpuTensor) -> GpuTensor:
@@ -386,12 +458,106 @@ def add_fp16_gpu(a: GpuTensor, b: GpuTensor) -> GpuTensor:
     return _to32(c16)
 
 
+# ------------------------------------------------- activations (any rank) --
+def _unary(name: str, entry: str, input: GpuTensor) -> GpuTensor:
+    _valid(name, input)
+    x = input.tensor
+    y = _new(x)
+    L.call(entry, x.data_ptr(), y.data_ptr(), x.numel(), L.ZK_F32, _stream(x))
+    return GpuTensor(y)
+
+
+def relu_gpu(input: GpuTensor) -> GpuTensor:
+    """max(x, 0) (bindings.cpp:1224-1246). Any rank: the reference's 4D
+    requirement comes from its cuDNN tensor descriptor, not from ReLU."""
+    return _unary("relu_gpu", "zk_relu", input)
+
+
+def sigmoid_gpu(input: GpuTensor) -> GpuTensor:
+    """1 / (1 + exp(-x)): the function the ONNX Sigmoid operator's GPU branch
+    calls (activation_ops.py:82-91); not bound in the reference."""
+    return _unary("sigmoid_gpu", "zk_sigmoid", input)
+
+
+def tanh_gpu(input: GpuTensor) -> GpuTensor:
+    """tanh(x): the function the ONNX Tanh operator's GPU branch calls
+    (activation_ops.py:111-120); not bound in the reference."""
+    return _unary("tanh_gpu", "zk_tanh", input)
+
+
+def add_gpu(a: GpuTensor, b: GpuTensor) -> GpuTensor:
+    """a + b for tensors of one shape (bindings.cpp:1313-1337; any rank, the
+    4D requirement there is cuDNN's)."""
+    _valid("add_gpu", a, b)
+    if a.shape != b.shape:
+        raise RuntimeError("add_gpu: shapes differ")
+    x, z = a.tensor, b.tensor
+    c = _new(x)
+    L.call("zk_add", x.data_ptr(), z.data_ptr(), c.data_ptr(), 1, x.numel(), 1, L.ZK_F32,
+           _stream(x))
+    return GpuTensor(c)
+
+
+# -------------------------------------------- NumPy-array interface ---
+# NumPy float32 in, NumPy float32 out; each call uploads its inputs, runs the
+# kernel and copies the result back (bindings.cpp:631-682, 842-870,
+# 1117-1150, 2010-2131).
+def _host(name: str, array, ndim: int | None) -> torch.Tensor:
+    if not torch.cuda.is_available():
+        raise RuntimeError(f"{name}: no GPU is visible")
+    a = np.ascontiguousarray(np.asarray(array, dtype=np.float32))
+    if ndim is not None and a.ndim != ndim:
+        raise RuntimeError(f"{name} requires a {ndim}D array")
+    return torch.from_numpy(a).to("cuda")
+
+
+def matmul(A, B) -> np.ndarray:
+    """C = A @ B for 2D float32 arrays (bindings.cpp:631-682)."""
+    a, b = _host("matmul", A, 2), _host("matmul", B, 2)
+    if a.shape[1] != b.shape[0]:
+        raise RuntimeError("Inner dimensions do not match")
+    return _matmul_nn(a, b).cpu().numpy()
+
+
+def add(a, b) -> np.ndarray:
+    """a + b for float32 arrays of one shape (bindings.cpp:1117-1150)."""
+    x, z = _host("add", a, None), _host("add", b, None)
+    if x.shape != z.shape:
+        raise RuntimeError("add requires arrays of one shape")
+    return add_gpu(GpuTensor(x), GpuTensor(z)).to_numpy()
+
+
+def relu(input) -> np.ndarray:
+    """max(x, 0) of a float32 array (bindings.cpp:842-870)."""
+    return relu_gpu(GpuTensor(_host("relu", input, None))).to_numpy()
+
+
+def gelu(input) -> np.ndarray:
+    """tanh GELU of a 2D float32 array (bindings.cpp:2017-2046)."""
+    return gelu_gpu(GpuTensor(_host("gelu", input, 2))).to_numpy()
+
+
+def layernorm(input, gamma, beta, eps: float = 1e-5) -> np.ndarray:
+    """LayerNorm over the last dim of a 2D float32 array (bindings.cpp:2050-2094)."""
+    x = _host("layernorm", input, 2)
+    g, b = _host("layernorm", gamma, None), _host("layernorm", beta, None)
+    return _layernorm(x, None, g, b, eps, L.ZK_F32).to_numpy()
+
+
+def softmax(input) -> np.ndarray:
+    """Row softmax of a 2D float32 array (bindings.cpp:2097-2131)."""
+    return softmax_gpu(GpuTensor(_host("softmax", input, 2))).to_numpy()
+
+
 __all__ = [
-    "GpuTensor", "to_gpu", "empty", "sync",
+    "GpuTensor", "to_gpu", "to_numpy", "empty", "sync", "is_available", "memory_stats",
+    "clear_memory_pool",
     "gelu_gpu", "layernorm_gpu", "matmul_gpu", "linear_gpu", "softmax_gpu",
     "flash_attention_gpu", "cublas_attention_gpu", "add_2d_gpu",
     "fused_add_layernorm_gpu", "fused_bias_gelu_gpu",
     "transpose_for_attention", "transpose_from_attention", "reshape_4d_to_2d",
     "attention_fp16_gpu", "attention_full_fp16_gpu", "linear_fp16_gpu",
     "gelu_fp16_gpu", "layernorm_fp16_gpu", "add_fp16_gpu",
+    "relu_gpu", "sigmoid_gpu", "tanh_gpu", "add_gpu",
+    "matmul", "add", "relu", "gelu", "layernorm", "softmax",
 ]

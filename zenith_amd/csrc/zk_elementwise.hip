@@ -1,4 +1,4 @@
-// Bandwidth-bound elementwise kernels: ReLU, (bias+)GELU, int8 quantisation
+// Bandwidth-bound elementwise kernels: ReLU, sigmoid, tanh, (bias+)GELU, int8 quantisation
 // and the fp16 transpose. Every kernel moves 16-byte vectors per lane where
 // the shape and alignment allow it and falls back to a scalar grid-stride
 // loop otherwise.
@@ -19,40 +19,65 @@ static inline int grid_for(int64_t work, int block) {
   return (int)g;
 }
 
-// ------------------------------------------------------------------ ReLU --
-template <typename T>
-__global__ void relu_vec(const T *__restrict__ x, T *__restrict__ y,
-                         int64_t nvec) {
+// ---------------------------------------------- ReLU, sigmoid, tanh --
+// One grid-stride kernel per op over 16-byte vectors, then a scalar tail.
+// fp16 values are computed in fp32 and rounded once. sigmoid is
+// 1 / (1 + expf(-x)) with the IEEE division (0 for x below about -88, 1
+// above about 17); tanh is the device library's tanhf.
+enum UnaryOp { kRelu = 0, kSigmoid = 1, kTanh = 2 };
+
+template <int OP>
+__device__ inline float unary(float v) {
+  if constexpr (OP == kRelu) return v > 0.f ? v : 0.f;
+  else if constexpr (OP == kSigmoid) return 1.0f / (1.0f + expf(-v));
+  else return tanhf(v);
+}
+
+template <int OP, typename T>
+__global__ void unary_vec(const T *__restrict__ x, T *__restrict__ y,
+                          int64_t nvec) {
   typedef typename Vec16<T>::type V;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nvec;
        i += stride) {
     V v = reinterpret_cast<const V *>(x)[i];
 #pragma unroll
-    for (int j = 0; j < Vec16<T>::n; ++j) v[j] = v[j] > (T)0 ? v[j] : (T)0;
+    for (int j = 0; j < Vec16<T>::n; ++j) v[j] = (T)unary<OP>((float)v[j]);
     reinterpret_cast<V *>(y)[i] = v;
   }
 }
 
-template <typename T>
-__global__ void relu_scalar(const T *__restrict__ x, T *__restrict__ y,
-                            int64_t begin, int64_t n) {
+template <int OP, typename T>
+__global__ void unary_scalar(const T *__restrict__ x, T *__restrict__ y,
+                             int64_t begin, int64_t n) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = begin + blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
        i < n; i += stride)
-    y[i] = x[i] > (T)0 ? x[i] : (T)0;
+    y[i] = (T)unary<OP>((float)x[i]);
 }
 
-template <typename T>
-static int relu_impl(const void *xv, void *yv, int64_t n, hipStream_t s) {
+template <int OP, typename T>
+static int unary_impl(const void *xv, void *yv, int64_t n, hipStream_t s,
+                      const char *name) {
   const T *x = (const T *)xv;
   T *y = (T *)yv;
   constexpr int W = Vec16<T>::n;
   int64_t nvec = (aligned16(x) && aligned16(y)) ? n / W : 0;
-  if (nvec > 0) relu_vec<T><<<grid_for(nvec, 256), 256, 0, s>>>(x, y, nvec);
+  if (nvec > 0) unary_vec<OP, T><<<grid_for(nvec, 256), 256, 0, s>>>(x, y, nvec);
   if (nvec * W < n)
-    relu_scalar<T><<<grid_for(n - nvec * W, 256), 256, 0, s>>>(x, y, nvec * W, n);
-  return check_launch("zk_relu");
+    unary_scalar<OP, T><<<grid_for(n - nvec * W, 256), 256, 0, s>>>(x, y, nvec * W, n);
+  return check_launch(name);
+}
+
+template <int OP>
+static int unary_entry(const void *x, void *y, int64_t n, int dtype, void *stream,
+                       const char *name) {
+  if (n < 0) return fail(ZK_ERR_INVALID, "%s: negative size", name);
+  if (n == 0) return ZK_OK;
+  if (!x || !y) return fail(ZK_ERR_INVALID, "%s: null pointer", name);
+  if (dtype == ZK_F32) return unary_impl<OP, float>(x, y, n, as_stream(stream), name);
+  if (dtype == ZK_F16) return unary_impl<OP, f16>(x, y, n, as_stream(stream), name);
+  return fail(ZK_ERR_UNSUPPORTED, "%s: dtype %d not supported", name, dtype);
 }
 
 // ------------------------------------------------------------------ GELU --
@@ -206,12 +231,17 @@ using namespace zk;
 
 extern "C" int zk_relu(const void *x, void *y, int64_t n, int dtype,
                        void *stream) {
-  if (n < 0) return fail(ZK_ERR_INVALID, "zk_relu: negative size");
-  if (n == 0) return ZK_OK;
-  if (!x || !y) return fail(ZK_ERR_INVALID, "zk_relu: null pointer");
-  if (dtype == ZK_F32) return relu_impl<float>(x, y, n, as_stream(stream));
-  if (dtype == ZK_F16) return relu_impl<f16>(x, y, n, as_stream(stream));
-  return fail(ZK_ERR_UNSUPPORTED, "zk_relu: dtype %d not supported", dtype);
+  return unary_entry<kRelu>(x, y, n, dtype, stream, "zk_relu");
+}
+
+extern "C" int zk_sigmoid(const void *x, void *y, int64_t n, int dtype,
+                          void *stream) {
+  return unary_entry<kSigmoid>(x, y, n, dtype, stream, "zk_sigmoid");
+}
+
+extern "C" int zk_tanh(const void *x, void *y, int64_t n, int dtype,
+                       void *stream) {
+  return unary_entry<kTanh>(x, y, n, dtype, stream, "zk_tanh");
 }
 
 extern "C" int zk_gelu(const void *x, const void *bias, void *y, int64_t rows,
