@@ -127,6 +127,19 @@ def test_flash_attention_cross_lengths(dev):
     assert ok, worst
 
 
+@pytest.mark.parametrize("Sk,lens", [(200, [150, 200, 0, 1]), (130, [130, 65, 129, 64])])
+def test_flash_attention_long_queries_ragged_keys(dev, Sk, lens):
+    """Sq >= 128 with Sk not a multiple of the 64-key tile: the last tile's
+    rows past Sk must read as zeros; lengths 0, 1, a tile boundary, Sk."""
+    q, _, _ = _qkv(4, 3, 128, 128, 64, tag=80)
+    _, k, v = _qkv(4, 3, Sk, Sk, 64, tag=85)
+    lens = np.array(lens, np.int32)
+    o = _run(dev, q, k, v, lens, torch.float16)
+    assert np.all(o[lens == 0] == 0)
+    ok, worst = fp16_tol(o, ops.attention(q, k, v, lens))
+    assert ok, worst
+
+
 @pytest.mark.parametrize("S", [128, 512])
 def test_flash_attention_deterministic(dev, S):
     """Repeated launches on the same inputs give bit-identical outputs (the

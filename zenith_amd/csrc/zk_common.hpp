@@ -18,6 +18,16 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+// Output stores are non-temporal (streaming): the written lines are not
+// kept in the writer's cache, which measured faster for every producer
+// here whose result is read by the next kernel (it is still served from
+// the memory-side cache) and for results written once.
+template <typename V>
+__device__ __forceinline__ void store_nt(V *p, V v) {
+  __builtin_nontemporal_store(v, p);
+}
 
 constexpr int kWave = 64;
 
@@ -101,6 +111,44 @@ __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
   return v;
+}
+
+// ------------------------------------------------------------ LDS DMA --
+// Buffer loads that write LDS directly (buffer_load ... lds) are counted by
+// vmcnt like any load. A ring of stages is consumed as: wait until the
+// stage about to be read has landed (leaving younger stages in flight),
+// then meet at lds_barrier.
+#define ZK_LDS(p) ((__attribute__((address_space(3))) void *)(p))
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Wait until at most min(allowed, N) slices of PER instructions each are
+// still in flight (allowed is wave-uniform).
+template <int N, int PER>
+__device__ __forceinline__ void wait_slices(int allowed) {
+  if constexpr (N == 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (allowed >= N) wait_vmcnt<N * PER>();
+    else wait_slices<N - 1, PER>(allowed);
+  }
+}
+// Workgroup barrier without the fence __syncthreads() carries: the fence
+// would make the compiler wait for every outstanding LDS DMA, including the
+// slices deliberately left in flight. Completion of the slice about to be
+// read is established by the explicit vmcnt wait before it.
+// The wave's own outstanding LDS reads are completed first, so that a
+// stage every wave has issued its last reads of is safe to refill after it.
+// (The wait is the compiler-visible builtin, simm16 0xC07F = lgkmcnt(0)
+// with vmcnt and expcnt left open, so the compiler knows those fragment
+// registers are ready and adds no later wait on younger reads.)
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // ------------------------------------------------------------------ MFMA --

@@ -43,7 +43,7 @@ __global__ void unary_vec(const T *__restrict__ x, T *__restrict__ y,
     V v = reinterpret_cast<const V *>(x)[i];
 #pragma unroll
     for (int j = 0; j < Vec16<T>::n; ++j) v[j] = (T)unary<OP>((float)v[j]);
-    reinterpret_cast<V *>(y)[i] = v;
+    store_nt(reinterpret_cast<V *>(y) + i, v);
   }
 }
 
@@ -116,7 +116,7 @@ __global__ __launch_bounds__(kGeluBlock) void gelu_rows(const T *__restrict__ x,
     V v[R];
 #pragma unroll
     for (int u = 0; u < R; ++u)
-      if (r0 + u < rows) v[u] = xv[(r0 + u) * ncv + cv];
+      if (r0 + u < rows) v[u] = __builtin_nontemporal_load(xv + (r0 + u) * ncv + cv);
 #pragma unroll
     for (int u = 0; u < R; ++u) {
       if (r0 + u < rows) {
@@ -127,7 +127,7 @@ __global__ __launch_bounds__(kGeluBlock) void gelu_rows(const T *__restrict__ x,
           if (BIAS) f += (float)b[j];
           o[j] = (T)gelu<T, MODE>(f);
         }
-        yv[(r0 + u) * ncv + cv] = o;
+        store_nt(yv + (r0 + u) * ncv + cv, o);
       }
     }
   }
@@ -191,7 +191,7 @@ __global__ void quant_f16_vec(const f16 *__restrict__ x, int8_t *__restrict__ q,
       lo |= (uint32_t)(uint8_t)quant1((float)v[j], scale, inv) << (8 * j);
       hi |= (uint32_t)(uint8_t)quant1((float)v[j + 4], scale, inv) << (8 * j);
     }
-    reinterpret_cast<uint2 *>(q)[i] = make_uint2(lo, hi);
+    store_nt(reinterpret_cast<u32x2 *>(q) + i, u32x2{lo, hi});
   }
 }
 

@@ -68,8 +68,6 @@ struct GemmParams {
   int64_t split_stride;
 };
 
-#define ZK_LDS(p) ((__attribute__((address_space(3))) void *)(p))
-
 // MFMA step on 16 bytes per lane and operand. MS = 32: lane l supplies row
 // l % 32, bytes [16 * (l / 32), +16) of the 32-byte k-step; the result
 // register r of lane l is D[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32].
@@ -215,37 +213,6 @@ struct GemmCfg {
   static_assert(SMEM <= 160 * 1024, "LDS budget");
   static_assert(WTN % 8 == 0, "epilogue vectors");
 };
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-// Wait until at most min(allowed, N) slices of PER instructions each are
-// still in flight (allowed is wave-uniform).
-template <int N, int PER>
-__device__ __forceinline__ void wait_slices(int allowed) {
-  if constexpr (N == 0) {
-    wait_vmcnt<0>();
-  } else {
-    if (allowed >= N) wait_vmcnt<N * PER>();
-    else wait_slices<N - 1, PER>(allowed);
-  }
-}
-// Workgroup barrier without the fence __syncthreads() carries: the fence
-// would make the compiler wait for every outstanding LDS DMA, including the
-// slices deliberately left in flight. Completion of the slice about to be
-// read is established by the explicit vmcnt wait before it.
-// The wave's own outstanding LDS reads are completed first, so that a
-// stage every wave has issued its last reads of is safe to refill after it.
-// (The wait is the compiler-visible builtin, simm16 0xC07F = lgkmcnt(0)
-// with vmcnt and expcnt left open, so the compiler knows those fragment
-// registers are ready and adds no later wait on younger reads.)
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xC07F);
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
 
 // Scheduling hint for one k-step: NR LDS fragment reads spread evenly over
 // NM MFMAs (a read, then its share of MFMAs), so read latency hides under
@@ -489,7 +456,7 @@ void gemm_mfma_kernel(GemmParams p) {
             f16x8 h;
 #pragma unroll
             for (int e = 0; e < 8; ++e) h[e] = (f16)o[e];
-            *(f16x8 *)dst = h;
+            store_nt((f16x8 *)dst, h);
           } else if constexpr (Q8) {
             uint32_t qlo = 0, qhi = 0;
 #pragma unroll
@@ -497,7 +464,7 @@ void gemm_mfma_kernel(GemmParams p) {
               qlo |= (uint32_t)(uint8_t)quant1((float)(f16)o[e], p.s_q, inv_q) << (8 * e);
               qhi |= (uint32_t)(uint8_t)quant1((float)(f16)o[e + 4], p.s_q, inv_q) << (8 * e);
             }
-            *(uint2 *)dst = make_uint2(qlo, qhi);
+            store_nt((u32x2 *)dst, u32x2{qlo, qhi});
           } else {
             *(f32x4 *)dst = f32x4{o[0], o[1], o[2], o[3]};
             *(f32x4 *)(dst + 4) = f32x4{o[4], o[5], o[6], o[7]};

@@ -93,7 +93,7 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
 #pragma unroll
       for (int j = 0; j < W; ++j)
         o[j] = (T)((v[k][j] - mean) * rstd * (float)g[j] + (float)b[j]);
-      yr[idx] = o;
+      store_nt(yr + idx, o);
       if constexpr (Q8) {
         static_assert(W == 8, "int8 output is written 8 bytes per vector");
         const float inv = 1.0f / qs;
@@ -103,7 +103,7 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
           lo |= (uint32_t)(uint8_t)quant1((float)o[j], qs, inv) << (8 * j);
           hi |= (uint32_t)(uint8_t)quant1((float)o[j + 4], qs, inv) << (8 * j);
         }
-        reinterpret_cast<uint2 *>(q + row * hidden)[idx] = make_uint2(lo, hi);
+        store_nt(reinterpret_cast<u32x2 *>(q + row * hidden) + idx, u32x2{lo, hi});
       }
     }
   }
