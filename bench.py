@@ -6,7 +6,9 @@ One step = one forward of the 12-layer encoder over one batch of 32
 sequences x 128 tokens (synthetic, seeded; key-padding lengths ~ U{64..128}),
 replayed from a HIP graph, inputs resident in HBM. Prints ONE JSON line with:
 
-  value / ms_per_step  fp16 encoder (the INT8-FFN variant in `int8_ffn`)
+  value / ms_per_step  fp16 encoder (the INT8-FFN variant in `int8_ffn`; the
+                       same fp16 encoder at seq 512, config 5's other
+                       length, in `encoder_s512`)
   roofline             the dominant kernel (FFN-up GEMM, 4096x768 -> 3072,
                        bias + erf-GELU epilogue, 2*M*N*K = 19.33 GFLOP per
                        launch) timed with HIP events around a HIP-graph
@@ -62,6 +64,7 @@ def _args():
     ap.add_argument("--no-int8", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
     ap.add_argument("--no-e4", action="store_true", help="skip the hybrid-API encoder (E4)")
+    ap.add_argument("--no-s512", action="store_true", help="skip the seq-512 encoder line")
     ap.add_argument("--only", default=None, help="launch one kernel --iters times and exit")
     ap.add_argument("--iters", type=int, default=20)
     return ap.parse_args()
@@ -450,6 +453,20 @@ def main():
         int8 = {"value": round(B * args.steps / dt8, 2),
                 "ms_per_step": round(dt8 / args.steps * 1e3, 4)}
         enc.disable_int8_ffn()
+    s512 = None
+    if not args.no_s512 and S != 512:
+        # config 5 also names seq 512: the same fp16 encoder, reported beside the headline
+        S2 = 512
+        gx2, gl2, go2 = enc.capture(B, S2)
+        gx2.copy_(torch.from_numpy(synthetic.hidden_states(B, S2, seed=43)).to(dev, torch.float16))
+        gl2.copy_(torch.from_numpy(synthetic.padding_lengths(B, S2)).to(dev))
+        steps2 = max(10, args.steps // 4)
+        dt2 = timed(steps2, max(2, args.warmup // 4))
+        assert torch.isfinite(go2.float()).all(), "non-finite encoder output (s512)"
+        fl2 = args.layers * (2 * B * S2 * 768 * (3 * 768 + 768 + 2 * 3072) + 4 * B * 12 * S2 * S2 * 64)
+        s512 = {"value": round(B * steps2 / dt2, 2), "unit": "seqs/s", "seq_len": S2,
+                "steps": steps2, "ms_per_step": round(dt2 / steps2 * 1e3, 4),
+                "encoder_tflops": round(fl2 * steps2 / dt2 / 1e12, 2)}
     del enc
     torch.cuda.empty_cache()
 
@@ -468,6 +485,7 @@ def main():
                    "global_batch": B, "seq_len": S, "parallelism": "none (1 GPU)"},
         "encoder_tflops": round(fwd_flops * args.steps / dt / 1e12, 2),
         "int8_ffn": int8,
+        "encoder_s512": s512,
         "roofline": {"bound": "mfma", "achieved": roof["achieved"], "peak": roof["peak"],
                      "unit": roof["unit"], "frac": roof["frac"], "traffic": pmc_traffic()},
         "roofline_kernel": {"kernel": "gemm_mfma_kernel<F16, bias+gelu_erf> M=4096 K=768 N=3072",
