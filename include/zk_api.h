@@ -237,6 +237,19 @@ int zk_gemm_f32_ws(const float *A, const float *B, float *C, int64_t M, int64_t 
                    int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_b,
                    void *workspace, int64_t ws_bytes, void *stream);
 
+/* Y[M,N] = epilogue(X[M,K] . W[N,K]^T) in fp32 (torch Linear layout), with
+ * the epilogues of zk_gemm_f16 (bias, bias+GELU erf / tanh, bias+residual,
+ * bias+ReLU; `bias` fp32 [N], `residual` fp32 [M, ldr]) fused into the GEMM
+ * (or into its split-K reduction) and an optional caller workspace as for
+ * zk_gemm_f32_ws. Replaces the fp32 linear of the GPU tensor API,
+ * linear_gpu (python/src/bindings.cpp:1454-1498: cuBLAS SGEMM, then a bias
+ * kernel) and zenith_cuda's fp32 Linear (cuda_bindings.cpp:73 matmul, then
+ * bias and activation kernels). */
+int zk_linear_f32(const float *X, const float *W, float *Y, int64_t M, int64_t N, int64_t K,
+                  int64_t ldx, int64_t ldw, int64_t ldy, const float *bias,
+                  const float *residual, int64_t ldr, int epilogue, void *workspace,
+                  int64_t ws_bytes, void *stream);
+
 /* Embedding gather, out[i, :] = table[ids[i], :] for int32 ids [n] and a
  * [vocab, hidden] table in dtype ZK_F32 or ZK_F16; an id outside [0, vocab)
  * gives a zero row. Replaces embedding_f32

@@ -55,6 +55,14 @@ def test_library_exports_every_declared_symbol():
                                        None, -1.0, L.ZK_F16, None), L.ZK_ERR_INVALID),
     (lambda lib: lib.zk_quantize_i8(16, 16, 4, 0.0, L.ZK_F32, None), L.ZK_ERR_INVALID),
     (lambda lib: lib.zk_transpose_f16(16, 16, 4, 8, 4, 4, None), L.ZK_ERR_INVALID),
+    (lambda lib: lib.zk_linear_f32(16, 16, 16, 8, 8, 8, 8, 8, 8, None, None, 0, 1, None, 0, None),
+     L.ZK_ERR_INVALID),  # bias epilogue without bias
+    (lambda lib: lib.zk_linear_f32(16, 16, 16, 8, 8, 8, 8, 8, 8, 16, None, 0, 4, None, 0, None),
+     L.ZK_ERR_INVALID),  # residual epilogue without residual
+    (lambda lib: lib.zk_linear_f32(16, 16, 16, 8, 8, 8, 8, 8, 8, 16, None, 0, 9, None, 0, None),
+     L.ZK_ERR_INVALID),  # unknown epilogue
+    (lambda lib: lib.zk_linear_f32(16, 16, 16, 8, 8, 8, 4, 8, 8, None, None, 0, 0, None, 0, None),
+     L.ZK_ERR_INVALID),  # ldx < K
 ])
 def test_argument_errors(call, code):
     lib = L.load()

@@ -214,3 +214,41 @@ def test_linear_split_k(dev, M, K, N, act):
     assert ok, worst
     for _ in range(3):
         assert torch.equal(zc.linear(*args, residual=res, **kw), y16)
+
+
+@pytest.mark.parametrize("M,K,N", [(128, 256, 192), (37, 70, 29), (16, 768, 768), (300, 768, 3072)])
+@pytest.mark.parametrize("epi", ["none", "bias", "gelu_erf", "gelu_tanh", "relu", "residual"])
+def test_linear_f32_c_abi(dev, M, K, N, epi):
+    """zk_linear_f32 through the C ABI on the three fp32 paths: the MFMA
+    kernel (K % 4 == 0), the SIMT kernel with its separate epilogue pass
+    (K = 70) and split-K with the epilogue in the ordered reduction (M = 16),
+    each epilogue against the float64 product; rtol 1e-4 (fp32 products and
+    accumulation; erf-GELU to 1.5e-7 of erf)."""
+    from zenith_amd import _lib as L
+    from zenith_amd.zenith_cuda import _ws_args, gemm_workspace
+
+    x = synthetic.normal((M, K), tag=60)
+    w = synthetic.normal((N, K), tag=61, std=0.05)
+    b = synthetic.normal((N,), tag=62)
+    r = synthetic.normal((M, N), tag=63)
+    code = {"none": L.ZK_EPI_NONE, "bias": L.ZK_EPI_BIAS, "gelu_erf": L.ZK_EPI_BIAS_GELU_ERF,
+            "gelu_tanh": L.ZK_EPI_BIAS_GELU_TANH, "relu": L.ZK_EPI_BIAS_RELU,
+            "residual": L.ZK_EPI_BIAS_RESIDUAL}[epi]
+    tx, tw, tb, tr = (_t(a, dev, torch.float32) for a in (x, w, b, r))
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    ws = gemm_workspace(M, N, K, L.ZK_F32, dev)
+    L.call("zk_linear_f32", tx.data_ptr(), tw.data_ptr(), y.data_ptr(), M, N, K, K, K, N,
+           None if epi == "none" else tb.data_ptr(), tr.data_ptr() if epi == "residual" else None,
+           N, code, *_ws_args(ws), torch.cuda.current_stream().cuda_stream)
+    ref = ops.matmul_f64(x, w.T)
+    if epi != "none":
+        ref = ref + b
+    if epi == "gelu_erf":
+        ref = ops.gelu_erf(ref.astype(np.float32))
+    elif epi == "gelu_tanh":
+        ref = ops.gelu_tanh(ref.astype(np.float32))
+    elif epi == "relu":
+        ref = ops.relu(ref)
+    elif epi == "residual":
+        ref = ref + r
+    np.testing.assert_allclose(y.cpu().numpy(), ref, rtol=1e-4, atol=1e-4)

@@ -285,12 +285,11 @@ def linear_gpu(X: GpuTensor, W: GpuTensor, bias: GpuTensor) -> GpuTensor:
     if w.shape[1] != K:
         raise RuntimeError("linear_gpu: W.dim(1) must match X.dim(1)")
     y = _new(x, (M, N))
-    s = _stream(x)
+    has_bias = isinstance(bias, GpuTensor) and bias.is_valid() and bias.dim(0) == N
     ws = gemm_workspace(M, N, K, L.ZK_F32, x.device)
-    L.call("zk_gemm_f32_ws", x.data_ptr(), w.data_ptr(), y.data_ptr(), M, N, K, K, K, N, 1,
-           *_ws_args(ws), s)
-    if isinstance(bias, GpuTensor) and bias.is_valid() and bias.dim(0) == N:
-        L.call("zk_add", y.data_ptr(), bias.tensor.data_ptr(), y.data_ptr(), M, N, 1, L.ZK_F32, s)
+    L.call("zk_linear_f32", x.data_ptr(), w.data_ptr(), y.data_ptr(), M, N, K, K, K, N,
+           bias.tensor.data_ptr() if has_bias else None, None, 0,
+           L.ZK_EPI_BIAS if has_bias else L.ZK_EPI_NONE, *_ws_args(ws), _stream(x))
     return GpuTensor(y)
 
 

@@ -841,28 +841,47 @@ extern "C" int zk_gemm_i8_requant(const int8_t *A, const int8_t *W, int8_t *Q, i
   return check_launch("zk_gemm_i8_requant");
 }
 
+// Epilogue of the SIMT fp32 path, in place on C: the same operations, in the
+// same order, as the MFMA kernel's epilogue.
+template <int EPI>
+__global__ __launch_bounds__(256) void f32_epilogue_kernel(float *__restrict__ C, int64_t ldc,
+                                                           int64_t M, int64_t N,
+                                                           const float *__restrict__ bias,
+                                                           const float *__restrict__ res,
+                                                           int64_t ldr) {
+  const int64_t total = M * N, stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t r = i / N, c = i % N;
+    float v = epilogue<EPI>(C[r * ldc + c], bias[c]);
+    if (EPI == ZK_EPI_BIAS_RESIDUAL) v += res[r * ldr + c];
+    C[r * ldc + c] = v;
+  }
+}
+
 static int gemm_f32_impl(const float *A, const float *B, float *C, int64_t M, int64_t N,
                          int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_b, void *ws,
-                         int64_t ws_bytes, void *stream) {
-  int st = check_dims("zk_gemm_f32", M, N, K);
+                         int64_t ws_bytes, void *stream, const float *bias = nullptr,
+                         const float *res = nullptr, int64_t ldr = 0, int epi = ZK_EPI_NONE,
+                         const char *who = "zk_gemm_f32") {
+  int st = check_dims(who, M, N, K);
   if (st) return st;
   if (M == 0 || N == 0) return ZK_OK;
-  if (!A || !B || !C) return fail(ZK_ERR_INVALID, "zk_gemm_f32: null pointer");
+  if (!A || !B || !C) return fail(ZK_ERR_INVALID, "%s: null pointer", who);
   if (lda < K || ldc < N || (trans_b ? ldb < K : ldb < N))
-    return fail(ZK_ERR_INVALID, "zk_gemm_f32: leading dimension too small");
+    return fail(ZK_ERR_INVALID, "%s: leading dimension too small", who);
   hipStream_t s = as_stream(stream);
   // W[N,K] operand with 16-byte rows: the MFMA kernel (fp32 matrix-core
   // products, fp32 accumulation); buffer offsets of a 256-row tile must fit
   // in 31 bits.
   if (trans_b && K > 0 && K % 4 == 0 && lda % 4 == 0 && ldb % 4 == 0 && aligned16(A) &&
       aligned16(B) && lda < (1 << 21) && ldb < (1 << 21)) {
-    GemmParams p{A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc, nullptr, nullptr, 0, 1.f, nullptr, 0};
+    GemmParams p{A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc, bias, res, ldr, 1.f, nullptr, 0};
     const SplitPlan sp = plan_split(M, N, K, 4);
     if (ws && sp.splits > 1 && ws_bytes >= split_ws_bytes(M, N, sp) && aligned16(ws))
-      launch_split<F32Op, float>(p, ZK_EPI_NONE, sp, (float *)ws, s);
+      launch_split<F32Op, float>(p, epi, sp, (float *)ws, s);
     else
-      launch_mfma<F32Op, float, false>(p, ZK_EPI_NONE, s);
-    return check_launch("zk_gemm_f32");
+      launch_mfma<F32Op, float, false>(p, epi, s);
+    return check_launch(who);
   }
   if ((M + 63) / 64 > 65535) return fail(ZK_ERR_UNSUPPORTED, "zk_gemm_f32: M too large");
   dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
@@ -870,7 +889,20 @@ static int gemm_f32_impl(const float *A, const float *B, float *C, int64_t M, in
     gemm_f32_kernel<true><<<grid, 256, 0, s>>>(A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc);
   else
     gemm_f32_kernel<false><<<grid, 256, 0, s>>>(A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc);
-  return check_launch("zk_gemm_f32");
+  if (epi != ZK_EPI_NONE) {
+    int64_t g = (M * N + 255) / 256;
+    if (g > 4096) g = 4096;
+#define ZK_E(E) f32_epilogue_kernel<E><<<(unsigned)g, 256, 0, s>>>(C, ldc, M, N, bias, res, ldr)
+    switch (epi) {
+      case ZK_EPI_BIAS: ZK_E(ZK_EPI_BIAS); break;
+      case ZK_EPI_BIAS_GELU_ERF: ZK_E(ZK_EPI_BIAS_GELU_ERF); break;
+      case ZK_EPI_BIAS_GELU_TANH: ZK_E(ZK_EPI_BIAS_GELU_TANH); break;
+      case ZK_EPI_BIAS_RESIDUAL: ZK_E(ZK_EPI_BIAS_RESIDUAL); break;
+      case ZK_EPI_BIAS_RELU: ZK_E(ZK_EPI_BIAS_RELU); break;
+    }
+#undef ZK_E
+  }
+  return check_launch(who);
 }
 
 extern "C" int zk_gemm_f32(const float *A, const float *B, float *C, int64_t M,
@@ -884,6 +916,21 @@ extern "C" int zk_gemm_f32_ws(const float *A, const float *B, float *C, int64_t 
                               void *workspace, int64_t ws_bytes, void *stream) {
   if (ws_bytes < 0) return fail(ZK_ERR_INVALID, "zk_gemm_f32_ws: negative workspace size");
   return gemm_f32_impl(A, B, C, M, N, K, lda, ldb, ldc, trans_b, workspace, ws_bytes, stream);
+}
+
+extern "C" int zk_linear_f32(const float *X, const float *W, float *Y, int64_t M, int64_t N,
+                             int64_t K, int64_t ldx, int64_t ldw, int64_t ldy,
+                             const float *bias, const float *residual, int64_t ldr,
+                             int epilogue, void *workspace, int64_t ws_bytes, void *stream) {
+  if (ws_bytes < 0) return fail(ZK_ERR_INVALID, "zk_linear_f32: negative workspace size");
+  if (epilogue < ZK_EPI_NONE || epilogue > ZK_EPI_BIAS_RELU)
+    return fail(ZK_ERR_INVALID, "zk_linear_f32: bad epilogue %d", epilogue);
+  if (epilogue != ZK_EPI_NONE && !bias)
+    return fail(ZK_ERR_INVALID, "zk_linear_f32: epilogue needs a bias");
+  if (epilogue == ZK_EPI_BIAS_RESIDUAL && (!residual || ldr < N))
+    return fail(ZK_ERR_INVALID, "zk_linear_f32: residual epilogue needs residual and ldr >= N");
+  return gemm_f32_impl(X, W, Y, M, N, K, ldx, ldw, ldy, 1, workspace, ws_bytes, stream, bias,
+                       residual, ldr, epilogue, "zk_linear_f32");
 }
 
 extern "C" int64_t zk_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int dtype) {

@@ -278,7 +278,7 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
     """y = act(x . weight^T + bias) [+ residual], torch Linear layout
     weight[N, K]. fp16 runs on the MFMA kernel with the epilogue fused
     (Linear+GELU: fused_gemm_epilogue_gelu, core/src/fused_kernels.cu:317-330);
-    fp32 runs the fp32 GEMM followed by the fused bias/activation kernels."""
+    fp32 runs zk_linear_f32, the fp32 GEMM with the same epilogues fused."""
     _need_cuda(x, weight, bias, residual)
     if weight.dim() != 2 or x.shape[-1] != weight.shape[1]:
         raise RuntimeError("linear: weight must be [out_features, in_features]")
@@ -315,29 +315,28 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
         return y.reshape(*lead, N)
     if x.dtype != torch.float32 or weight.dtype != torch.float32:
         raise RuntimeError("linear expects float32 or float16 tensors")
+    b = bias
+    if b is None and (activation is not None or residual is not None):
+        b = torch.zeros(N, dtype=torch.float32, device=x.device)
+    if b is not None:
+        if b.numel() != N:
+            raise RuntimeError("linear: bias must be [out_features]")
+        b = b.to(torch.float32).contiguous()
+    epi = L.ZK_EPI_NONE if b is None else _ACT_EPI[activation]
+    res2 = None
+    if residual is not None:
+        res2 = residual.reshape(-1, N).to(torch.float32).contiguous()
+        if res2.shape[0] != x2.shape[0]:
+            raise RuntimeError("linear: residual must be [..., out_features]")
+        epi = L.ZK_EPI_BIAS_RESIDUAL
     x2 = x2.contiguous()
     w = weight.contiguous()
     M = x2.shape[0]
     y = torch.empty((M, N), dtype=torch.float32, device=x.device)
     if M:
         ws = gemm_workspace(M, N, K, L.ZK_F32, x.device)
-        L.call("zk_gemm_f32_ws", _p(x2), _p(w), _p(y), M, N, K, K, K, N, 1, *_ws_args(ws),
-               _stream(x2))
-    if bias is not None:
-        if activation in ("gelu", "gelu_erf", "gelu_tanh"):
-            y = bias_gelu(y, bias.contiguous(),
-                          approximate="tanh" if activation == "gelu_tanh" else "none")
-        else:
-            if M:
-                L.call("zk_add", _p(y), _p(bias.to(torch.float32).contiguous()), _p(y), M, N, 1,
-                       L.ZK_F32, _stream(y))
-            if activation == "relu":
-                y = relu(y)
-    elif activation is not None:
-        y = gelu(y, "tanh" if activation == "gelu_tanh" else "none") if activation != "relu" else relu(y)
-    if residual is not None and M:
-        r = residual.reshape(-1, N).to(torch.float32).contiguous()
-        L.call("zk_add", _p(y), _p(r), _p(y), M, N, M, L.ZK_F32, _stream(y))
+        L.call("zk_linear_f32", _p(x2), _p(w), _p(y), M, N, K, K, K, N, _p(b), _p(res2), N, epi,
+               *_ws_args(ws), _stream(x2))
     return y.reshape(*lead, N)
 
 
