@@ -46,11 +46,20 @@ __device__ __forceinline__ f16x4 lds_read_tr16(const f16 *p) {
   return __builtin_bit_cast(f16x4, v);
 }
 
+// D = 64 K/V tiles are stored as unpadded 128-byte rows with 16-byte chunk c
+// of row r in slot c ^ kv_swz(r): a K fragment read (16 rows, one chunk per
+// 16-lane group) and a transposing V read (4 rows x 4 chunks per 32 lanes)
+// then both hit 64 distinct banks, which no uniform row padding achieves.
+__device__ __forceinline__ int kv_swz(int r) {
+  return ((r & 2) << 1) | ((r & 4) >> 1) | ((r >> 3) & 1);
+}
+
 template <int D, int NW>
 __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
   constexpr int KT = 64;
   constexpr int NT = NW * 64;
-  constexpr int KLD = D + 8;   // K and V tile row pitch (halves)
+  constexpr bool SWZ = D == 64;  // swizzled unpadded rows (else padded rows)
+  constexpr int KLD = SWZ ? D : D + 8;  // K and V tile row pitch (halves)
   constexpr int DV = D / 8;    // 16-byte vectors per K/V row
   constexpr int PER = KT * DV / NT;
   static_assert(KT * DV % NT == 0, "tile/thread mismatch");
@@ -98,8 +107,9 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
 #pragma unroll
     for (int v = 0; v < PER; ++v) {
       const int idx = tid + v * NT;
-      *(f16x8 *)(Ks + (idx / DV) * KLD + (idx % DV) * 8) = kr[v];
-      *(f16x8 *)(Vs + (idx / DV) * KLD + (idx % DV) * 8) = vr[v];
+      const int row = idx / DV, ch = SWZ ? (idx % DV) ^ kv_swz(row) : idx % DV;
+      *(f16x8 *)(Ks + row * KLD + ch * 8) = kr[v];
+      *(f16x8 *)(Vs + row * KLD + ch * 8) = vr[v];
     }
   };
 
@@ -118,7 +128,8 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
       for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
 #pragma unroll
       for (int c = 0; c < D / 16; ++c) {
-        const f16x8 kf = *(const f16x8 *)(Ks + (kb * 32 + (lane & 31)) * KLD + c * 16 + h32 * 8);
+        const int kch = SWZ ? (2 * c + h32) ^ kv_swz(lane & 31) : 2 * c + h32;
+        const f16x8 kf = *(const f16x8 *)(Ks + (kb * 32 + (lane & 31)) * KLD + kch * 8);
         s[kb] = mfma32x32x16(kf, qf[c], s[kb]);
       }
     }
@@ -174,17 +185,22 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
     // i % 4 of the 4 elements read by source lane 4*j + i/4. Source lane s
     // therefore reads key k0 + s/4, dims dbase + 4*(s%4), and output lane i
     // gets dim dbase + i at keys k0 .. k0+3.
+    // (with SWZ: chunk ch of row r0 + 32 kb + 16 c2 sits in slot ch ^ kv_swz(r0),
+    // and of the row 8 further in slot ch ^ kv_swz(r0) ^ 1)
     const int grp = lane >> 4, sl = lane & 15;
-    const f16 *vsrc = Vs + (4 * (grp >> 1) + (sl >> 2)) * KLD + 16 * (grp & 1) + 4 * (sl & 3);
+    const int r0 = 4 * (grp >> 1) + (sl >> 2);
+    const int fv = SWZ ? kv_swz(r0) : 0;
+    const int vch = 2 * (grp & 1) + ((sl & 3) >> 1), vin = 4 * (sl & 1);
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2) {
-          const f16 *src = vsrc + (kb * 32 + c2 * 16) * KLD + dt * 32;
-          const f16x4 lo = lds_read_tr16(src);
-          const f16x4 hi = lds_read_tr16(src + 8 * KLD);
+          const f16 *row = Vs + (r0 + kb * 32 + c2 * 16) * KLD;
+          const int ch = 4 * dt + vch;
+          const f16x4 lo = lds_read_tr16(row + (((ch ^ fv) << 3) + vin));
+          const f16x4 hi = lds_read_tr16(row + 8 * KLD + (((ch ^ (SWZ ? fv ^ 1 : 0)) << 3) + vin));
           const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
           o[dt] = mfma32x32x16(vf, pf[kb][c2], o[dt]);
         }
