@@ -140,6 +140,21 @@ def test_matmul_fp32(dev, M, K, N):
     np.testing.assert_allclose(c.cpu().numpy(), ops.matmul_f64(a, b), rtol=1e-5, atol=1e-4)
 
 
+def test_matmul_fp32_strided_b(dev):
+    """B[K,N] read through a row stride wider than N (a column slice): the
+    transpose + fp32 MFMA route (K % 4 == 0, large enough) copies it dense
+    first; the SIMT route reads it by stride."""
+    from zenith_amd import zenith_cuda as zc
+
+    for M, K, N in ((256, 512, 384), (9, 10, 11)):
+        a = synthetic.uniform((M, K), tag=13)
+        big = synthetic.uniform((K, N + 12), tag=14)
+        tb = _t(big, dev, torch.float32)[:, 5:5 + N]
+        c = zc.matmul(_t(a, dev, torch.float32), tb)
+        np.testing.assert_allclose(c.cpu().numpy(), ops.matmul_f64(a, big[:, 5:5 + N]),
+                                   rtol=1e-5, atol=1e-4)
+
+
 @pytest.mark.parametrize("M,K,N", [
     (4100, 72, 4100),   # 8-wave 256x256 tile
     (4000, 100, 2000),  # 8-wave 256x192 tile

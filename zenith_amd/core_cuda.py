@@ -41,7 +41,7 @@ import numpy as np
 import torch
 
 from . import _lib as L
-from .zenith_cuda import _pad_k, _ws_args, gemm_workspace
+from .zenith_cuda import _gemm_f32_nn, _pad_k, _ws_args, gemm_workspace
 
 F32, F16 = torch.float32, torch.float16
 
@@ -251,26 +251,8 @@ def matmul_gpu(A: GpuTensor, B: GpuTensor) -> GpuTensor:
     return GpuTensor(_matmul_nn(A.tensor, B.tensor))
 
 
-# Products of at least this many multiply-adds transpose B once and run on
-# the fp32 MFMA GEMM (which reads B as [N, K]); smaller ones, and K not a
-# multiple of 4, take the SIMT kernel in one launch.
-_MFMA_MIN_MACS = 1 << 18
-
-
 def _matmul_nn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-    M, K = a.shape
-    N = b.shape[1]
-    c = _new(a, (M, N))
-    s = _stream(a)
-    if K % 4 == 0 and M * N * K >= _MFMA_MIN_MACS:
-        bt = _new(b, (N, K))
-        L.call("zk_transpose_0213", b.data_ptr(), bt.data_ptr(), 1, K, N, 1, L.ZK_F32, s)
-        ws = gemm_workspace(M, N, K, L.ZK_F32, a.device)
-        L.call("zk_gemm_f32_ws", a.data_ptr(), bt.data_ptr(), c.data_ptr(), M, N, K, K, K, N, 1,
-               *_ws_args(ws), s)
-    else:
-        L.call("zk_gemm_f32", a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K, K, N, N, 0, s)
-    return c
+    return _gemm_f32_nn(a, b)
 
 
 def linear_gpu(X: GpuTensor, W: GpuTensor, bias: GpuTensor) -> GpuTensor:

@@ -251,15 +251,36 @@ def matmul(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
         return wmma_matmul(A, B, out_dtype=torch.float16)
     if A.dtype != torch.float32 or B.dtype != torch.float32:
         raise RuntimeError("matmul expects two float32 (or two float16) tensors")
-    M, K = A.shape
-    N = B.shape[1]
     A = A if A.stride(1) == 1 else A.contiguous()
     B = B if B.stride(1) == 1 else B.contiguous()
+    return _gemm_f32_nn(A, B)
+
+
+# fp32 products of at least this many multiply-adds (and K % 4 == 0) transpose
+# B once into W[N, K] and run on the fp32 MFMA GEMM, 2-5x the SIMT kernel's
+# rate on B[K, N]; smaller ones take the SIMT kernel in one launch.
+_F32_MFMA_MIN_MACS = 1 << 18
+
+
+def _gemm_f32_nn(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
+    """C[M,N] = A[M,K] . B[K,N] in fp32 (row-major, unit column stride)."""
+    M, K = A.shape
+    N = B.shape[1]
     C = torch.empty((M, N), dtype=torch.float32, device=A.device)
     if M == 0 or N == 0:
         return C
-    L.call("zk_gemm_f32", _p(A), _p(B), _p(C), M, N, K, max(A.stride(0), K),
-           max(B.stride(0), N), C.stride(0), 0, _stream(A))
+    s = _stream(A)
+    lda, ldb = max(A.stride(0), K), max(B.stride(0), N)
+    if K % 4 == 0 and M * N * K >= _F32_MFMA_MIN_MACS:
+        bt = torch.empty((N, K), dtype=torch.float32, device=A.device)
+        if ldb == N:
+            L.call("zk_transpose_0213", _p(B), _p(bt), 1, K, N, 1, L.ZK_F32, s)
+        else:  # strided rows: transpose the dense copy
+            L.call("zk_transpose_0213", _p(B.contiguous()), _p(bt), 1, K, N, 1, L.ZK_F32, s)
+        ws = gemm_workspace(M, N, K, L.ZK_F32, A.device)
+        L.call("zk_gemm_f32_ws", _p(A), _p(bt), _p(C), M, N, K, lda, K, N, 1, *_ws_args(ws), s)
+    else:
+        L.call("zk_gemm_f32", _p(A), _p(B), _p(C), M, N, K, lda, ldb, N, 0, s)
     return C
 
 
