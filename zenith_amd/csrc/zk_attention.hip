@@ -16,6 +16,9 @@
 // query with no valid key produces 0 (mask rule of the reference's masked
 // attention primitive).
 //
+// For D = 64 and at most 128 queries, fa_fwd_f16_q16_kernel below does the
+// same arithmetic with 16 queries per wavefront on 16x16x32 MFMAs.
+//
 // fp32 path (SIMT): D/32 lanes per query, each holding 32 dims of q and of
 // the output accumulator; K/V tiles in LDS are read as broadcasts.
 #include "zk_common.hpp"
@@ -220,6 +223,152 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
   }
 }
 
+// fp16, D = 64, 16 queries per wavefront on 16x16x32 MFMAs, NW wavefronts
+// per workgroup. Same arithmetic as fa_fwd_f16_kernel (fp32 statistics, exp2
+// with the scale folded in, lazy rescaling, P rounded to fp16), with half
+// the per-wavefront dependency chain and twice the wavefronts.
+// S^T = K . Q^T: lane l supplies K[key 16 kb + l%16][dims 8 (l/16) + 32 ks ..]
+// and Q[query l%16][same dims], and receives S^T[16 kb + 4 (l/16) + r][l%16].
+// O^T += V^T . P^T over 32 keys per step: k-slot 8 g + j (g = l / 16) is key
+// 4 g + j for j < 4 and 16 + 4 g + (j - 4) otherwise, so the B operand is the
+// lane's own probabilities of key blocks 2 st and 2 st + 1, and the V^T
+// operand comes from two transposing reads 16 keys apart.
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void fa_fwd_f16_q16_kernel(AttnParams p) {
+  constexpr int D = 64, KT = 64, NT = NW * 64, DV = D / 8;
+  constexpr int PER = KT * DV / NT;
+  static_assert(KT * DV % NT == 0 && PER >= 1, "tile/thread mismatch");
+  __shared__ __attribute__((aligned(16))) f16 Ks[KT * D];
+  __shared__ __attribute__((aligned(16))) f16 Vs[KT * D];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int L = valid_len(p, b);
+  const f16 *Qb = (const f16 *)p.Q + b * p.sq[0] + h * p.sq[1];
+  const f16 *Kb = (const f16 *)p.K + b * p.sk[0] + h * p.sk[1];
+  const f16 *Vb = (const f16 *)p.V + b * p.sv[0] + h * p.sv[1];
+  f16 *Ob = (f16 *)p.O + b * p.so[0] + h * p.so[1];
+
+  const int qrow = blockIdx.x * (NW * 16) + wave * 16 + c16;
+  const bool qvalid = qrow < p.Sq;
+  f16x8 qf[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+    qf[ks] = qvalid ? *(const f16x8 *)(Qb + qrow * p.sq[2] + 32 * ks + 8 * g)
+                    : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+
+  f32x4 o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -__builtin_inff(), l = 0.f;
+
+  const int ntiles = (L + KT - 1) / KT;
+  f16x8 kr[PER], vr[PER];
+  auto load_kv = [&](int t) {
+#pragma unroll
+    for (int v = 0; v < PER; ++v) {
+      const int idx = tid + v * NT;
+      const int kk = t * KT + idx / DV;
+      kr[v] = kk < p.Sk ? *(const f16x8 *)(Kb + kk * p.sk[2] + (idx % DV) * 8)
+                        : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      vr[v] = kk < p.Sk ? *(const f16x8 *)(Vb + kk * p.sv[2] + (idx % DV) * 8)
+                        : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  };
+  auto stash_kv = [&]() {
+#pragma unroll
+    for (int v = 0; v < PER; ++v) {
+      const int idx = tid + v * NT;
+      const int row = idx / DV, ch = (idx % DV) ^ kv_swz(idx / DV);
+      *(f16x8 *)(Ks + row * D + ch * 8) = kr[v];
+      *(f16x8 *)(Vs + row * D + ch * 8) = vr[v];
+    }
+  };
+  // V^T source address of this lane: key 4 g + l%16 / 4 (+ 32 st, + 16),
+  // dims 16 db + 4 (l % 4); with the swizzle, chunk 2 db + (l%4)/2 of a row
+  // r is in slot chunk ^ kv_swz(r), and kv_swz ignores the +32 st / +16.
+  const int r0 = 4 * g + (c16 >> 2);
+  const int fv = kv_swz(r0), vhalf = (c16 & 3) >> 1, vin = 4 * (c16 & 1);
+
+  if (ntiles > 0) load_kv(0);
+  for (int t = 0; t < ntiles; ++t) {
+    __syncthreads();
+    stash_kv();
+    __syncthreads();
+    if (t + 1 < ntiles) load_kv(t + 1);
+
+    f32x4 s4[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      s4[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int row = 16 * kb + c16;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const f16x8 kf = *(const f16x8 *)(Ks + row * D + (((4 * ks + g) ^ kv_swz(row)) << 3));
+        s4[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], s4[kb], 0, 0, 0);
+      }
+    }
+    if (t * KT + KT > L) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (t * KT + 16 * kb + 4 * g + r >= L) s4[kb][r] = -__builtin_inff();
+    }
+    float tmax = -__builtin_inff();
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+      tmax = fmaxf(tmax, fmaxf(fmaxf(s4[kb][0], s4[kb][1]), fmaxf(s4[kb][2], s4[kb][3])));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * p.scale_log2;  // finite: key t*KT < L
+    if (__builtin_amdgcn_ballot_w64(tmax > m + 8.0f) != 0) {
+      const float m_new = fmaxf(m, tmax);
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+      m = m_new;
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[db][r] *= alpha;
+    }
+    float psum = 0.f;
+    f16x8 pf[2];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float e = __builtin_amdgcn_exp2f(fmaf(s4[kb][r], p.scale_log2, -m));
+        psum += e;
+        pf[kb >> 1][4 * (kb & 1) + r] = (f16)e;
+      }
+    psum += __shfl_xor(psum, 16, 64);
+    psum += __shfl_xor(psum, 32, 64);
+    l += psum;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const f16 *row = Vs + (32 * st + r0) * D + ((((2 * db + vhalf) ^ fv)) << 3) + vin;
+        const f16x4 lo = lds_read_tr16(row);
+        const f16x4 hi = lds_read_tr16(row + 16 * D);
+        const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[st], o[db], 0, 0, 0);
+      }
+  }
+
+  if (qvalid) {
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      f16x4 out;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) out[r] = (f16)(o[db][r] * inv);
+      *(f16x4 *)(Ob + qrow * p.so[2] + 16 * db + 4 * g) = out;
+    }
+  }
+}
+
 // ---------------------------------------------------------------- fp32 ----
 template <int D>
 __global__ __launch_bounds__(256) void fa_fwd_f32_kernel(AttnParams p) {
@@ -292,6 +441,17 @@ template <int D>
 static void launch_f16(const AttnParams &p, hipStream_t s) {
   // 4 wavefronts x 32 queries per workgroup: at seq 128 one workgroup holds a
   // whole (batch, head), so K and V are read from HBM once.
+  // Up to 128 queries (BERT s128), D = 64: 16-query wavefronts, 4 per
+  // workgroup. The shorter per-wave chain and the doubled wave count win
+  // where the kernel is latency-bound (encoder 1.4185 -> 1.3818 ms per step at
+  // b32 s128); at s512 the 32-query kernel's lower LDS traffic per query wins.
+  if constexpr (D == 64) {
+    if (p.Sq <= 128) {
+      dim3 grid((unsigned)((p.Sq + 63) / 64), (unsigned)p.H, (unsigned)p.B);
+      fa_fwd_f16_q16_kernel<4><<<grid, 256, 0, s>>>(p);
+      return;
+    }
+  }
   if (p.Sq >= 128) {
     dim3 grid((unsigned)((p.Sq + 127) / 128), (unsigned)p.H, (unsigned)p.B);
     fa_fwd_f16_kernel<D, 4><<<grid, 256, 0, s>>>(p);
