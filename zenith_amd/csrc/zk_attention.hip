@@ -233,13 +233,13 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
 // 4 g + j for j < 4 and 16 + 4 g + (j - 4) otherwise, so the B operand is the
 // lane's own probabilities of key blocks 2 st and 2 st + 1, and the V^T
 // operand comes from two transposing reads 16 keys apart.
-template <int NW>
+template <int NW, int TPS = 1>
 __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_q16_kernel(AttnParams p) {
   constexpr int D = 64, KT = 64, NT = NW * 64, DV = D / 8;
-  constexpr int PER = KT * DV / NT;
-  static_assert(KT * DV % NT == 0 && PER >= 1, "tile/thread mismatch");
-  __shared__ __attribute__((aligned(16))) f16 Ks[KT * D];
-  __shared__ __attribute__((aligned(16))) f16 Vs[KT * D];
+  constexpr int PER = TPS * KT * DV / NT;  // TPS key tiles per LDS stage
+  static_assert(TPS * KT * DV % NT == 0 && PER >= 1, "tile/thread mismatch");
+  __shared__ __attribute__((aligned(16))) f16 Ks[TPS * KT * D];
+  __shared__ __attribute__((aligned(16))) f16 Vs[TPS * KT * D];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c16 = lane & 15;
@@ -264,12 +264,13 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_q16_kernel(AttnParams p) {
   float m = -__builtin_inff(), l = 0.f;
 
   const int ntiles = (L + KT - 1) / KT;
+  const int nstages = (ntiles + TPS - 1) / TPS;
   f16x8 kr[PER], vr[PER];
-  auto load_kv = [&](int t) {
+  auto load_kv = [&](int stg) {
 #pragma unroll
     for (int v = 0; v < PER; ++v) {
       const int idx = tid + v * NT;
-      const int kk = t * KT + idx / DV;
+      const int kk = stg * TPS * KT + idx / DV;
       kr[v] = kk < p.Sk ? *(const f16x8 *)(Kb + kk * p.sk[2] + (idx % DV) * 8)
                         : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
       vr[v] = kk < p.Sk ? *(const f16x8 *)(Vb + kk * p.sv[2] + (idx % DV) * 8)
@@ -291,70 +292,76 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_q16_kernel(AttnParams p) {
   const int r0 = 4 * g + (c16 >> 2);
   const int fv = kv_swz(r0), vhalf = (c16 & 3) >> 1, vin = 4 * (c16 & 1);
 
-  if (ntiles > 0) load_kv(0);
-  for (int t = 0; t < ntiles; ++t) {
+  if (nstages > 0) load_kv(0);
+  for (int stg = 0; stg < nstages; ++stg) {
     __syncthreads();
     stash_kv();
     __syncthreads();
-    if (t + 1 < ntiles) load_kv(t + 1);
+    if (stg + 1 < nstages) load_kv(stg + 1);
+    for (int sub = 0; sub < TPS; ++sub) {
+      const int t = stg * TPS + sub;
+      if (t >= ntiles) break;  // wave-uniform; no barrier in this loop
+      const f16 *Kt = Ks + sub * KT * D;
+      const f16 *Vt = Vs + sub * KT * D;
 
-    f32x4 s4[4];
+      f32x4 s4[4];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      s4[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const int row = 16 * kb + c16;
+      for (int kb = 0; kb < 4; ++kb) {
+        s4[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const int row = 16 * kb + c16;
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const f16x8 kf = *(const f16x8 *)(Ks + row * D + (((4 * ks + g) ^ kv_swz(row)) << 3));
-        s4[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], s4[kb], 0, 0, 0);
+        for (int ks = 0; ks < 2; ++ks) {
+          const f16x8 kf = *(const f16x8 *)(Kt + row * D + (((4 * ks + g) ^ kv_swz(row)) << 3));
+          s4[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], s4[kb], 0, 0, 0);
+        }
       }
-    }
-    if (t * KT + KT > L) {
+      if (t * KT + KT > L) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (t * KT + 16 * kb + 4 * g + r >= L) s4[kb][r] = -__builtin_inff();
+      }
+      float tmax = -__builtin_inff();
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+        tmax = fmaxf(tmax, fmaxf(fmaxf(s4[kb][0], s4[kb][1]), fmaxf(s4[kb][2], s4[kb][3])));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * p.scale_log2;  // finite: key t*KT < L
+      if (__builtin_amdgcn_ballot_w64(tmax > m + 8.0f) != 0) {
+        const float m_new = fmaxf(m, tmax);
+        const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+        m = m_new;
+        l *= alpha;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[db][r] *= alpha;
+      }
+      float psum = 0.f;
+      f16x8 pf[2];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (t * KT + 16 * kb + 4 * g + r >= L) s4[kb][r] = -__builtin_inff();
-    }
-    float tmax = -__builtin_inff();
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-      tmax = fmaxf(tmax, fmaxf(fmaxf(s4[kb][0], s4[kb][1]), fmaxf(s4[kb][2], s4[kb][3])));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * p.scale_log2;  // finite: key t*KT < L
-    if (__builtin_amdgcn_ballot_w64(tmax > m + 8.0f) != 0) {
-      const float m_new = fmaxf(m, tmax);
-      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-      m = m_new;
-      l *= alpha;
+        for (int r = 0; r < 4; ++r) {
+          const float e = __builtin_amdgcn_exp2f(fmaf(s4[kb][r], p.scale_log2, -m));
+          psum += e;
+          pf[kb >> 1][4 * (kb & 1) + r] = (f16)e;
+        }
+      psum += __shfl_xor(psum, 16, 64);
+      psum += __shfl_xor(psum, 32, 64);
+      l += psum;
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o[db][r] *= alpha;
+        for (int st = 0; st < 2; ++st) {
+          const f16 *row = Vt + (32 * st + r0) * D + ((((2 * db + vhalf) ^ fv)) << 3) + vin;
+          const f16x4 lo = lds_read_tr16(row);
+          const f16x4 hi = lds_read_tr16(row + 16 * D);
+          const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[st], o[db], 0, 0, 0);
+        }
     }
-    float psum = 0.f;
-    f16x8 pf[2];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float e = __builtin_amdgcn_exp2f(fmaf(s4[kb][r], p.scale_log2, -m));
-        psum += e;
-        pf[kb >> 1][4 * (kb & 1) + r] = (f16)e;
-      }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
-    l += psum;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        const f16 *row = Vs + (32 * st + r0) * D + ((((2 * db + vhalf) ^ fv)) << 3) + vin;
-        const f16x4 lo = lds_read_tr16(row);
-        const f16x4 hi = lds_read_tr16(row + 16 * D);
-        const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[st], o[db], 0, 0, 0);
-      }
   }
 
   if (qvalid) {
@@ -447,8 +454,10 @@ static void launch_f16(const AttnParams &p, hipStream_t s) {
   // b32 s128); at s512 the 32-query kernel's lower LDS traffic per query wins.
   if constexpr (D == 64) {
     if (p.Sq <= 128) {
+      // both 64-key tiles of a 128-key sequence in one LDS stage: one load
+      // latency instead of two (encoder 1.424 -> 1.408 ms per step)
       dim3 grid((unsigned)((p.Sq + 63) / 64), (unsigned)p.H, (unsigned)p.B);
-      fa_fwd_f16_q16_kernel<4><<<grid, 256, 0, s>>>(p);
+      fa_fwd_f16_q16_kernel<4, 2><<<grid, 256, 0, s>>>(p);
       return;
     }
   }
