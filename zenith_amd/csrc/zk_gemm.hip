@@ -545,8 +545,7 @@ static int forced_cfg() {
   return forced >= 0 && forced < kNumCfgs ? forced : -1;
 }
 
-// kbytes: bytes of one row of A (K x element size).
-static int pick_cfg(int M, int N, int64_t kbytes) {
+static int pick_cfg(int M, int N, int K) {
   if (forced_cfg() >= 0) return forced_cfg();
   const int64_t tm256 = (M + 255) / 256;
   if (M >= 1024 && N > 1024 && tm256 * ((N + 255) / 256) >= 256) return 0;
@@ -556,9 +555,11 @@ static int pick_cfg(int M, int N, int64_t kbytes) {
   // small tiles below)
   const int64_t t192 = tm256 * ((N + 191) / 192);
   if (M >= 1024 && t192 >= 256) return 5;
-  // the 3-stage 128x128 ring for long rows (fp16 FFN-down, 6 KB); 64x64
-  // otherwise (int8 FFN-down's 3 KB rows: 16.3 us against 18.0)
-  if (N <= 1024) return kbytes >= 4096 ? 4 : 3;
+  // the 3-stage 128x128 ring for deep K (FFN-down, K = 3072, fp16 and int8),
+  // 64x64 otherwise. Timed alone, the int8 FFN-down is faster on 64x64 (16.3
+  // against 18.0 us), but inside the encoder 128x128 wins (INT8-FFN encoder
+  // 1.212 against 1.234 ms per step), so the encoder's figure decides.
+  if (N <= 1024) return K >= 2048 ? 4 : 3;
   if (M >= 1024 && t192 >= 160) return 5;
   const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
   return t128 >= 640 ? 1 : 2;
@@ -566,7 +567,7 @@ static int pick_cfg(int M, int N, int64_t kbytes) {
 
 template <class OP, typename OutT, bool DEQ>
 static void launch_mfma(GemmParams p, int epi, hipStream_t s, int cfg = -1) {
-  switch (cfg >= 0 ? cfg : pick_cfg(p.M, p.N, (int64_t)p.K * OP::kElem)) {
+  switch (cfg >= 0 ? cfg : pick_cfg(p.M, p.N, p.K)) {
     case 0: launch_epi<OP, 256, 256, 32, 128, 2, OutT, DEQ, 2, 4>(p, epi, s); break;
     case 1: launch_epi<OP, 128, 128, 32, 128, 2, OutT, DEQ>(p, epi, s); break;
     case 2: launch_epi<OP, 128, 96, 16, 128, 2, OutT, DEQ>(p, epi, s); break;
