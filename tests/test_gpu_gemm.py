@@ -92,7 +92,7 @@ def test_linear_epilogues(dev, act, M, K, N):
     (4000, 100, 2000),  # 8-wave 256x192 tile, vector stores
     (520, 200, 20500),  # 128x128, 2-stage ring
     (700, 136, 1100),   # 128x96, 16x16 MFMA
-    (1000, 3000, 600),  # 128x128, 3-stage ring (long K)
+    (1000, 3000, 600),  # 128x96, 4x1 waves, 3-stage ring (long K)
     (333, 500, 1000),   # 64x64, 16x16 MFMA
 ])
 def test_linear_tile_configs(dev, M, K, N):
@@ -160,7 +160,7 @@ def test_matmul_fp32_strided_b(dev):
     (4000, 100, 2000),  # 8-wave 256x192 tile
     (520, 200, 20500),  # 128x128, 2-stage ring
     (700, 136, 1100),   # 128x96, 16x16x4 fp32 MFMA
-    (1000, 3000, 600),  # 128x128, 3-stage ring
+    (1000, 3000, 600),  # 128x96, 4x1 waves, 3-stage ring
     (333, 500, 1000),   # 64x64
     (128, 768, 3072),   # the hybrid encoder's FFN-up shape
     (77, 70, 33),       # K % 4 != 0: the SIMT kernel

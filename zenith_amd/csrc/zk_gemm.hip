@@ -493,7 +493,7 @@ void gemm_mfma_kernel(GemmParams p) {
 //   1: 128x128, 32x32, 128-byte slices, 2-stage ring (2 WG/CU)
 //   2: 128x96,  16x16, 128-byte slices, 2-stage ring (2 WG/CU)
 //   3: 64x64,   16x16, 128-byte slices, 2-stage ring (up to 5 WG/CU)
-//   4: 128x128, 32x32, 128-byte slices, 3-stage ring (1 WG/CU)
+//   4: 128x96,  32x32, 128-byte slices, 3-stage ring, 4 waves (4 x 1)
 //   5: 256x192, 32x32, 128-byte slices, 2-stage ring, 8 waves (4 x 2)
 // The 8-wave tiles put two wavefronts of one workgroup on every SIMD, so
 // one wave's barrier or memory wait is covered by the other's MFMAs.
@@ -531,7 +531,8 @@ static void launch_epi(GemmParams p, int epi, hipStream_t s) {
 //   M >= 1024 and >= 256 tiles of 256x256 (4096^3 and up): the 8-wave
 //     256x256 tile;
 //   N <= 1024 (out-projection, FFN-down): 64x64 tiles for short K keep every
-//     CU busy; for K >= 2048 the 3-stage 128x128 ring hides more latency;
+//     CU busy; for K >= 2048 the 3-stage 128x96 ring (M = 4096, N = 768:
+//     256 tiles, one per CU);
 //   M >= 1024 and >= 160 tiles of 256x192 (FFN-up: 256, QKV: 192): the
 //     8-wave 256x192 tile;
 //   otherwise 128x128 once that gives >= 640 tiles, else 128x96.
@@ -555,10 +556,13 @@ static int pick_cfg(int M, int N, int K) {
   // small tiles below)
   const int64_t t192 = tm256 * ((N + 191) / 192);
   if (M >= 1024 && t192 >= 256) return 5;
-  // the 3-stage 128x128 ring for deep K (FFN-down, K = 3072, fp16 and int8),
-  // 64x64 otherwise. Timed alone, the int8 FFN-down is faster on 64x64 (16.3
-  // against 18.0 us), but inside the encoder 128x128 wins (INT8-FFN encoder
-  // 1.212 against 1.234 ms per step), so the encoder's figure decides.
+  // the 3-stage 128x96 ring for deep K (FFN-down, K = 3072, fp16 and int8),
+  // 64x64 otherwise. At M = 4096, N = 768 the 128x96 tile gives 256 tiles
+  // (one per CU) where 128x128 left 64 CUs idle: fp16 encoder 1.344 -> 1.306
+  // ms per step, INT8-FFN 1.165 -> 1.147. Timed alone, the int8 FFN-down is
+  // faster on 64x64 than on the 128x128 ring (16.3 against 18.0 us), but
+  // inside the encoder the ring won (1.212 against 1.234 ms per step), so
+  // encoder figures decide.
   if (N <= 1024) return K >= 2048 ? 4 : 3;
   if (M >= 1024 && t192 >= 160) return 5;
   const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
@@ -571,7 +575,7 @@ static void launch_mfma(GemmParams p, int epi, hipStream_t s, int cfg = -1) {
     case 0: launch_epi<OP, 256, 256, 32, 128, 2, OutT, DEQ, 2, 4>(p, epi, s); break;
     case 1: launch_epi<OP, 128, 128, 32, 128, 2, OutT, DEQ>(p, epi, s); break;
     case 2: launch_epi<OP, 128, 96, 16, 128, 2, OutT, DEQ>(p, epi, s); break;
-    case 4: launch_epi<OP, 128, 128, 32, 128, 3, OutT, DEQ>(p, epi, s); break;
+    case 4: launch_epi<OP, 128, 96, 32, 128, 3, OutT, DEQ, 4, 1>(p, epi, s); break;
     case 5: launch_epi<OP, 256, 192, 32, 128, 2, OutT, DEQ, 4, 2>(p, epi, s); break;
     default: launch_epi<OP, 64, 64, 16, 128, 2, OutT, DEQ>(p, epi, s); break;
   }
