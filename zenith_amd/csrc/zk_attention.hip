@@ -57,6 +57,19 @@ __device__ __forceinline__ int kv_swz(int r) {
   return ((r & 2) << 1) | ((r & 4) >> 1) | ((r >> 3) & 1);
 }
 
+// The 16-query kernel's transposing V read gives each 16-lane group 4 rows x
+// 2 chunks (group g: rows 4g .. 4g+3), and the LDS serves a 64-bit read in
+// two passes, one pairing the groups (0, 2) and (1, 3). kv_swz puts rows r
+// and r + 8 in the same slots, which costs each such read an extra pass.
+// kv_swz16 keeps the two chunks of a row in one aligned slot pair 2h, 2h+1
+// with h distinct over the even (and the odd) rows of groups {0,1}, {2,3},
+// {0,2} and {1,3}, and (h, low bit) distinct over all 16 rows for the K
+// fragment reads. LDS bank-conflict cycles of the b32 s128 launch: 1.97e5
+// with kv_swz, 0 with kv_swz16 (the encoder's time is unchanged).
+__device__ __forceinline__ int kv_swz16(int r) {
+  return 2 * (((r >> 1) & 3) ^ ((r >> 2) & 2)) + ((r >> 3) & 1);
+}
+
 template <int D, int NW>
 __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
   constexpr int KT = 64;
@@ -281,16 +294,16 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_q16_kernel(AttnParams p) {
 #pragma unroll
     for (int v = 0; v < PER; ++v) {
       const int idx = tid + v * NT;
-      const int row = idx / DV, ch = (idx % DV) ^ kv_swz(idx / DV);
+      const int row = idx / DV, ch = (idx % DV) ^ kv_swz16(idx / DV);
       *(f16x8 *)(Ks + row * D + ch * 8) = kr[v];
       *(f16x8 *)(Vs + row * D + ch * 8) = vr[v];
     }
   };
   // V^T source address of this lane: key 4 g + l%16 / 4 (+ 32 st, + 16),
   // dims 16 db + 4 (l % 4); with the swizzle, chunk 2 db + (l%4)/2 of a row
-  // r is in slot chunk ^ kv_swz(r), and kv_swz ignores the +32 st / +16.
+  // r is in slot chunk ^ kv_swz16(r), and kv_swz16 ignores the +32 st / +16.
   const int r0 = 4 * g + (c16 >> 2);
-  const int fv = kv_swz(r0), vhalf = (c16 & 3) >> 1, vin = 4 * (c16 & 1);
+  const int fv = kv_swz16(r0), vhalf = (c16 & 3) >> 1, vin = 4 * (c16 & 1);
 
   if (nstages > 0) load_kv(0);
   for (int stg = 0; stg < nstages; ++stg) {
@@ -311,7 +324,7 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_q16_kernel(AttnParams p) {
         const int row = 16 * kb + c16;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          const f16x8 kf = *(const f16x8 *)(Kt + row * D + (((4 * ks + g) ^ kv_swz(row)) << 3));
+          const f16x8 kf = *(const f16x8 *)(Kt + row * D + (((4 * ks + g) ^ kv_swz16(row)) << 3));
           s4[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], s4[kb], 0, 0, 0);
         }
       }
