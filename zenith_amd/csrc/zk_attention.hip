@@ -40,6 +40,23 @@ __device__ __forceinline__ int valid_len(const AttnParams &p, int b) {
   return L < 0 ? 0 : (L > p.Sk ? p.Sk : L);
 }
 
+// (query block, head, batch) of this workgroup. The gridDim.x query blocks of
+// one (batch, head) read the same K and V. Workgroups go to the 8 XCDs
+// round-robin by linear id, so when B*H is a multiple of 8 the blocks of one
+// head are given ids 8 apart: they run on one XCD and share its L2. At b32
+// s128 this cut the L2-miss reads from 31.5 MB to 18.9 MB (Q, K and V once).
+struct AttnTile {
+  int qb, h, b;
+};
+__device__ __forceinline__ AttnTile attn_tile() {
+  const int gx = gridDim.x, nh = gridDim.y, nbh = gridDim.y * gridDim.z;
+  if (gx == 1 || nbh % 8 != 0) return {(int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z};
+  const int bid = blockIdx.x + gx * (blockIdx.y + nh * blockIdx.z);
+  const int grp = bid / (8 * gx), rem = bid % (8 * gx);
+  const int bh = grp * 8 + rem % 8;
+  return {rem / 8, bh % nh, bh / nh};
+}
+
 // ds_read_b64_tr_b16: 8 bytes per lane, transposed across each group of 16
 // lanes (see its use below for the lane mapping).
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -83,14 +100,15 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) f16 Vs[KT * KLD];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h32 = lane >> 5;
-  const int b = blockIdx.z, h = blockIdx.y;
+  const AttnTile tile = attn_tile();
+  const int b = tile.b, h = tile.h;
   const int L = valid_len(p, b);
   const f16 *Qb = (const f16 *)p.Q + b * p.sq[0] + h * p.sq[1];
   const f16 *Kb = (const f16 *)p.K + b * p.sk[0] + h * p.sk[1];
   const f16 *Vb = (const f16 *)p.V + b * p.sv[0] + h * p.sv[1];
   f16 *Ob = (f16 *)p.O + b * p.so[0] + h * p.so[1];
 
-  const int qrow = blockIdx.x * (NW * 32) + wave * 32 + (lane & 31);
+  const int qrow = tile.qb * (NW * 32) + wave * 32 + (lane & 31);
   const bool qvalid = qrow < p.Sq;
   f16x8 qf[D / 16];
 #pragma unroll
@@ -256,14 +274,15 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_q16_kernel(AttnParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c16 = lane & 15;
-  const int b = blockIdx.z, h = blockIdx.y;
+  const AttnTile tile = attn_tile();
+  const int b = tile.b, h = tile.h;
   const int L = valid_len(p, b);
   const f16 *Qb = (const f16 *)p.Q + b * p.sq[0] + h * p.sq[1];
   const f16 *Kb = (const f16 *)p.K + b * p.sk[0] + h * p.sk[1];
   const f16 *Vb = (const f16 *)p.V + b * p.sv[0] + h * p.sv[1];
   f16 *Ob = (f16 *)p.O + b * p.so[0] + h * p.so[1];
 
-  const int qrow = blockIdx.x * (NW * 16) + wave * 16 + c16;
+  const int qrow = tile.qb * (NW * 16) + wave * 16 + c16;
   const bool qvalid = qrow < p.Sq;
   f16x8 qf[2];
 #pragma unroll
