@@ -49,12 +49,12 @@ struct AttnTile {
   int qb, h, b;
 };
 __device__ __forceinline__ AttnTile attn_tile() {
-  const int gx = gridDim.x, nh = gridDim.y, nbh = gridDim.y * gridDim.z;
+  const int64_t gx = gridDim.x, nh = gridDim.y, nbh = nh * gridDim.z;
   if (gx == 1 || nbh % 8 != 0) return {(int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z};
-  const int bid = blockIdx.x + gx * (blockIdx.y + nh * blockIdx.z);
-  const int grp = bid / (8 * gx), rem = bid % (8 * gx);
-  const int bh = grp * 8 + rem % 8;
-  return {rem / 8, bh % nh, bh / nh};
+  const int64_t bid = blockIdx.x + gx * (blockIdx.y + nh * blockIdx.z);
+  const int64_t grp = bid / (8 * gx), rem = bid % (8 * gx);
+  const int64_t bh = grp * 8 + rem % 8;
+  return {(int)(rem / 8), (int)(bh % nh), (int)(bh / nh)};
 }
 
 // ds_read_b64_tr_b16: 8 bytes per lane, transposed across each group of 16
