@@ -80,7 +80,8 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 //   erf(z) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-z^2),
 //   t = 1 / (1 + p z), |error| <= 1.5e-7.
 // With z = |x| / sqrt(2) and h = (1 - erf(z)) / 2 (the halves folded into
-// the a_k): GELU(x) = x (1 - h) for x >= 0 and x h for x < 0.
+// the a_k): GELU(x) = x (1 - h) for x >= 0 and x h for x < 0, which are both
+// max(x, 0) - |x| h (a max and one fma instead of a select).
 __device__ __forceinline__ float gelu_erf_fast(float x) {
   const float t = __builtin_amdgcn_rcpf(fmaf(fabsf(x), 0.3275911f * 0.70710678118654752f, 1.0f));
   float q = 0.5f * 1.061405429f;
@@ -90,7 +91,7 @@ __device__ __forceinline__ float gelu_erf_fast(float x) {
   q = fmaf(q, t, 0.5f * 0.254829592f);
   // exp(-z^2) = exp2(-x^2 log2(e) / 2)
   const float h = q * t * __builtin_amdgcn_exp2f(x * x * (-0.5f * 1.4426950408889634f));
-  return x * (x >= 0.f ? 1.0f - h : h);
+  return fmaf(-fabsf(x), h, fmaxf(x, 0.f));
 }
 // tanh(y) = 1 - 2 / (1 + exp(2y)) (exact identity), so
 // 0.5 x (1 + tanh(y)) = x - x / (1 + exp(2y)), y = sqrt(2/pi) (x + 0.044715 x^3).
