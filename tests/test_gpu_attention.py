@@ -35,9 +35,13 @@ def _run(dev, q, k, v, lens, dtype):
 
 
 @pytest.mark.parametrize("B,H,S,D", [(2, 12, 128, 64), (2, 3, 512, 64), (3, 2, 77, 64),
-                                     (2, 2, 130, 128), (2, 2, 64, 32), (1, 1, 1, 64)])
+                                     (2, 2, 130, 128), (2, 2, 64, 32), (1, 1, 1, 64),
+                                     (2, 4, 300, 64), (4, 2, 100, 64)])
 @pytest.mark.parametrize("masked", [False, True])
 def test_flash_attention_f16(dev, B, H, S, D, masked):
+    """B*H a multiple of 8 with 2 and 3 query blocks per head exercises the
+    workgroup remap that puts the blocks of one head on one XCD; B*H = 6 or 4
+    keeps the direct order."""
     q, k, v = _qkv(B, H, S, S, D)
     lens = None
     if masked:
