@@ -558,8 +558,9 @@ static int pick_cfg(int M, int N, int K) {
   if (M >= 1024 && t192 >= 256) return 5;
   // the 3-stage 128x96 ring for deep K (FFN-down, K = 3072, fp16 and int8),
   // 64x64 otherwise. At M = 4096, N = 768 the 128x96 tile gives 256 tiles
-  // (one per CU) where 128x128 left 64 CUs idle: fp16 encoder 1.344 -> 1.306
-  // ms per step, INT8-FFN 1.165 -> 1.147. Timed alone, the int8 FFN-down is
+  // (one per CU) where 128x128 left 64 CUs idle: the fp16 encoder is 1.8-2.8%
+  // and the INT8-FFN encoder 0.5-1.5% faster per step (one-process A/Bs in
+  // both orders, identical output). Timed alone, the int8 FFN-down is
   // faster on 64x64 than on the 128x128 ring (16.3 against 18.0 us), but
   // inside the encoder the ring won (1.212 against 1.234 ms per step), so
   // encoder figures decide.
