@@ -482,14 +482,16 @@ static void launch_f16(const AttnParams &p, hipStream_t s) {
   // whole (batch, head), so K and V are read from HBM once.
   // Up to 128 queries (BERT s128), D = 64: 16-query wavefronts, 4 per
   // workgroup. The shorter per-wave chain and the doubled wave count win
-  // where the kernel is latency-bound (encoder 1.4185 -> 1.3818 ms per step at
-  // b32 s128); at s512 the 32-query kernel's lower LDS traffic per query wins.
+  // where the kernel is latency-bound (encoder 0.5% faster per step at b32
+  // s128); at s512 the 32-query kernel's lower LDS traffic per query wins.
   if constexpr (D == 64) {
     if (p.Sq <= 128) {
-      // both 64-key tiles of a 128-key sequence in one LDS stage: one load
-      // latency instead of two (encoder 1.424 -> 1.408 ms per step)
+      // one 64-key tile per LDS stage, the next one loading under the
+      // current one's MFMAs. Staging both tiles of a 128-key sequence at once
+      // (TPS = 2) was 0.7% slower per encoder step, fp16 and INT8-FFN, in
+      // both-order A/Bs on two boxes.
       dim3 grid((unsigned)((p.Sq + 63) / 64), (unsigned)p.H, (unsigned)p.B);
-      fa_fwd_f16_q16_kernel<4, 2><<<grid, 256, 0, s>>>(p);
+      fa_fwd_f16_q16_kernel<4, 1><<<grid, 256, 0, s>>>(p);
       return;
     }
   }
