@@ -9,17 +9,19 @@ replayed from a HIP graph, inputs resident in HBM. Prints ONE JSON line with:
   value / ms_per_step  fp16 encoder (the INT8-FFN variant in `int8_ffn`; the
                        same fp16 encoder at seq 512, config 5's other
                        length, in `encoder_s512`)
-  roofline             the dominant kernel (FFN-up GEMM, 4096x768 -> 3072,
-                       bias + erf-GELU epilogue, 2*M*N*K = 19.33 GFLOP per
-                       launch) timed with HIP events around a HIP-graph
-                       replay of back-to-back launches on that stream;
-                       `traffic` from the rocprofv3 FETCH_SIZE / WRITE_SIZE
-                       summary in profiles/gemm_ffn_up_pmc.md when present
+  roofline             the dominant kernel of the timed step: the longest of
+                       the kernels one encoder layer launches (QKV, attention,
+                       out-projection, Add+LN, FFN-up, FFN-down), as measured
+                       in the `kernels` table (HIP events on the launch
+                       stream); `traffic` from its rocprofv3 FETCH_SIZE /
+                       WRITE_SIZE summary profiles/<name>_pmc.md when present
   kernels              per-kernel times and roofline fractions for the
                        workload configs: FP16 GEMM sweep (config 2), flash
                        attention s128 / s512 (config 3), INT8 FFN GEMMs
-                       (config 4), Add+LayerNorm and bias+GELU (HBM, buffer
-                       sets rotated past the 256 MB MALL)
+                       (config 4), Add+LayerNorm and bias+GELU at the s128
+                       and s512 sizes (HBM, buffer sets rotated past the
+                       256 MB MALL), each beside a plain copy of the same
+                       byte count
   e4_hybrid            the reference's published BERT comparator workload
                        (hybrid encoder on the GpuTensor API, b1 s128, timed
                        as the reference times it) beside its 9.74 ms (T4)
@@ -122,6 +124,11 @@ def _rc(L, rc):
         raise RuntimeError(L.last_error())
 
 
+def _log(msg: str) -> None:
+    """Progress line on stderr (stdout carries only the JSON line)."""
+    print(f"bench.py: {msg}", file=sys.stderr, flush=True)
+
+
 # ----------------------------------------------------------- kernel cases --
 def kernel_cases(torch, dev):
     """name -> (setup() -> (launch(i), work, unit, peak_key, bound, shape)).
@@ -186,9 +193,9 @@ def kernel_cases(torch, dev):
                 f"B={B} H={H} S={S} D={D} lens~U{{S/2..S}} (dense FLOPs)"
         return setup
 
-    def add_ln():
+    def add_ln(M=4096):
         def setup():
-            M, H = 4096, 768
+            H = 768
             per = 3 * M * H * 2
             n = max(2, (512 << 20) // per + 1)  # rotate past the 256 MB MALL
             xs = [torch.randn(M, H, device=dev, dtype=f16) for _ in range(n)]
@@ -207,9 +214,9 @@ def kernel_cases(torch, dev):
                 f"[{M},{H}] fp16, {n} rotating buffer sets"
         return setup
 
-    def bias_gelu():
+    def bias_gelu(M=4096):
         def setup():
-            M, N = 4096, 3072
+            N = 3072
             per = 2 * M * N * 2
             n = max(2, (512 << 20) // per + 1)
             xs = [torch.randn(M, N, device=dev, dtype=f16) for _ in range(n)]
@@ -236,6 +243,28 @@ def kernel_cases(torch, dev):
                     and keep), float(4 * n), "GB/s", "hbm", "hbm", "256 MB read + 256 MB write"
         return setup
 
+    def copy_like(total_bytes):
+        """Plain vector copy (the ReLU kernel: 16-byte loads and non-temporal
+        stores, no arithmetic to speak of) moving `total_bytes` per launch,
+        half read and half written, over rotating buffers past the MALL: what
+        a memory-bound kernel of that size can reach on this box."""
+        def setup():
+            n = int(total_bytes // 4)  # fp16 elements each way
+            n -= n % 8
+            per = 4 * n
+            k = max(2, (512 << 20) // per + 1)
+            xs = [torch.ones(n, device=dev, dtype=f16) for _ in range(k)]
+            ys = [torch.empty(n, device=dev, dtype=f16) for _ in range(k)]
+            keep = (xs, ys)
+
+            def launch(i):
+                j = i % k
+                _rc(L, lib.zk_relu(xs[j].data_ptr(), ys[j].data_ptr(), n, L.ZK_F16, s()))
+                return keep
+            return launch, float(per), "GB/s", "hbm", "hbm", \
+                f"{per / 2**20:.1f} MiB per launch (half read, half written), {k} rotating sets"
+        return setup
+
     del np
     E = L.ZK_EPI_BIAS
     return {
@@ -252,8 +281,29 @@ def kernel_cases(torch, dev):
         "int8_ffn_down": gemm_i8(4096, 3072, 768, E),
         "add_layernorm": add_ln(),
         "bias_gelu": bias_gelu(),
+        # config 5 at seq 512 (M = 32 x 512): the sizes where the HBM target
+        # is physically testable, each beside a copy of the same byte count
+        "add_layernorm_s512": add_ln(16384),
+        "bias_gelu_s512": bias_gelu(16384),
+        "copy_18.9MB": copy_like(3 * 4096 * 768 * 2),
+        "copy_50.3MB": copy_like(2 * 4096 * 3072 * 2),
+        "copy_75.5MB": copy_like(3 * 16384 * 768 * 2),
+        "copy_201MB": copy_like(2 * 16384 * 3072 * 2),
         "copy": copy(),
     }
+
+# kernels one step of the timed encoder (b32 s128) launches, per layer: the
+# roofline line names the longest of them
+STEP_KERNELS = ("gemm_qkv", "attn_s128", "gemm_out_proj", "add_layernorm", "gemm_ffn_up",
+                "gemm_ffn_down")
+KERNEL_DESC = {
+    "gemm_qkv": "gemm_mfma_kernel<F16Op, bias> M=4096 K=768 N=2304 (QKV)",
+    "gemm_out_proj": "gemm_mfma_kernel<F16Op, bias> M=4096 K=768 N=768 (out-projection)",
+    "gemm_ffn_up": "gemm_mfma_kernel<F16Op, bias+gelu_erf> M=4096 K=768 N=3072 (FFN-up)",
+    "gemm_ffn_down": "gemm_mfma_kernel<F16Op, bias> M=4096 K=3072 N=768 (FFN-down)",
+    "attn_s128": "fa_fwd_f16_q16_kernel B=32 H=12 S=128 D=64, key padding",
+    "add_layernorm": "ln_wave_kernel fp16 [4096,768] with residual",
+}
 
 
 def measure_kernels(torch, dev, names=None):
@@ -275,11 +325,11 @@ def measure_kernels(torch, dev, names=None):
     return out
 
 
-def pmc_traffic():
-    """HBM bytes per launch of the FFN-up GEMM from the committed rocprofv3
-    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel
-    calibration); None when the summary is absent."""
-    path = os.path.join(ROOT, "profiles", "gemm_ffn_up_pmc.md")
+def pmc_traffic(name: str):
+    """HBM bytes per launch of kernel case `name` from its committed
+    rocprofv3 counter summary profiles/<name>_pmc.md (FETCH_SIZE + WRITE_SIZE,
+    each scaled by the copy-kernel calibration); None when it is absent."""
+    path = os.path.join(ROOT, "profiles", f"{name}_pmc.md")
     try:
         txt = open(path).read()
     except OSError:
@@ -370,7 +420,83 @@ def cpu_baseline(seq: int, layers: int, budget_s: float):
         "sample": f"{done} sequences x {seq} tokens through {layers} fp32 layers "
                   f"(numpy oracle, {blas} BLAS, {threads} threads), {el:.1f} s; "
                   f"host cpus={len(os.sched_getaffinity(0))}",
+        "host": _host_info(),
+        "avx2_gemm": cpu_avx2_gemm(),
+        "config1_layer": cpu_config1_layer(),
     }
+
+
+def _host_info():
+    import numpy as np
+
+    model = "unknown"
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+        flags = open("/proc/cpuinfo").read()
+    except OSError:  # pragma: no cover
+        flags = ""
+    return {"cpu_model": model, "affinity_cpus": len(os.sched_getaffinity(0)),
+            "os_cpu_count": os.cpu_count(), "numpy": np.__version__,
+            "avx2": " avx2" in flags, "avx512f": " avx512f" in flags}
+
+
+def cpu_avx2_gemm():
+    """The reference's own CPU GEMM, matmul_f32_avx2 (core/src/cpu_kernels.cpp:
+    129-165, single-threaded i-k-j with 8-wide FMA), compiled from the
+    reference's source into oracle/_ref and timed on the config-2 BERT
+    shapes (M = 4096; one run each after a 256-row warm-up). Falls back to
+    the build's restatement (oracle/cpu_gemm.c) when oracle/_ref is absent."""
+    import numpy as np
+
+    from oracle import native
+
+    kind = "reference" if native.ref_available() else "port"
+    g = native.ref_gemm() if kind == "reference" else native.own_gemm()
+    rows = []
+    tot_f, tot_t = 0.0, 0.0
+    for M, K, N, name in ((4096, 768, 2304, "qkv"), (4096, 768, 768, "out_proj"),
+                          (4096, 768, 3072, "ffn_up"), (4096, 3072, 768, "ffn_down")):
+        rng = np.random.default_rng([42, M, K, N])
+        a = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+        b = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+        g.matmul(a[:256], b, "avx2")
+        t0 = time.perf_counter()
+        g.matmul(a, b, "avx2")
+        dt = time.perf_counter() - t0
+        fl = 2.0 * M * N * K
+        tot_f += fl
+        tot_t += dt
+        rows.append({"shape": f"{name} M={M} K={K} N={N}", "s": round(dt, 4),
+                     "gflops": round(fl / dt / 1e9, 2)})
+    return {"kind": kind, "cores": 1, "unit": "GFLOP/s", "value": round(tot_f / tot_t / 1e9, 2),
+            "sample": "config-2 BERT GEMM shapes (M=4096), one fp32 run each, single thread",
+            "shapes": rows}
+
+
+def cpu_config1_layer(runs: int = 5, warmup: int = 2):
+    """Config 1: one fp32 BERT layer, b1 s128, no mask, through the numpy
+    oracle; median of `runs` after `warmup`."""
+    import numpy as np
+
+    from oracle import bert as obert
+    from zenith_amd import synthetic
+
+    w = synthetic.bert_weights(1, seed=42)
+    x = synthetic.hidden_states(1, 128, seed=42)
+    for _ in range(warmup):
+        obert.bert_encoder(x, w)
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        obert.bert_encoder(x, w)
+        ts.append(time.perf_counter() - t0)
+    ms = float(np.median(ts)) * 1e3
+    return {"kind": "port", "median_ms": round(ms, 3), "runs": runs, "warmup": warmup,
+            "gflops": round(1.862 / (ms / 1e3), 2),
+            "sample": "one BERT-base layer fp32, b1 s128 (1.862 GFLOP), numpy oracle"}
 
 
 def _calibrate(enc, x, lens, torch):
@@ -438,12 +564,14 @@ def main():
         torch.cuda.synchronize()
         return time.perf_counter() - t0
 
+    _log(f"fp16 encoder b{B} s{S}: {args.steps} timed replays")
     dt = timed(args.steps, args.warmup)
     seqs_s = B * args.steps / dt
     assert torch.isfinite(go.float()).all(), "non-finite encoder output"
 
     int8 = None
     if not args.no_int8:
+        _log("INT8-FFN encoder")
         s_x, s_h = _calibrate(enc, x, lens, torch)
         enc.enable_int8_ffn(s_x, s_h, layers_fp32=layers)
         enc.capture(B, S)
@@ -457,6 +585,7 @@ def main():
     if not args.no_s512 and S != 512:
         # config 5 also names seq 512: the same fp16 encoder, reported beside the headline
         S2 = 512
+        _log("seq-512 encoder (fp16, INT8-FFN)")
         gx2, gl2, go2 = enc.capture(B, S2)
         gx2.copy_(torch.from_numpy(synthetic.hidden_states(B, S2, seed=43)).to(dev, torch.float16))
         gl2.copy_(torch.from_numpy(synthetic.padding_lengths(B, S2)).to(dev))
@@ -467,12 +596,31 @@ def main():
         s512 = {"value": round(B * steps2 / dt2, 2), "unit": "seqs/s", "seq_len": S2,
                 "steps": steps2, "ms_per_step": round(dt2 / steps2 * 1e3, 4),
                 "encoder_tflops": round(fl2 * steps2 / dt2 / 1e12, 2)}
+        if not args.no_int8:
+            # the INT8-FFN variant at seq 512, calibrated on its own input
+            x2 = gx2.clone()
+            l2 = gl2.clone()
+            s_x2, s_h2 = _calibrate(enc, x2, l2, torch)
+            enc.enable_int8_ffn(s_x2, s_h2, layers_fp32=layers)
+            enc.capture(B, S2)
+            enc._gx.copy_(x2)
+            enc._gl.copy_(l2)
+            dt28 = timed(steps2, max(2, args.warmup // 4))
+            assert torch.isfinite(enc._go.float()).all(), "non-finite INT8 encoder output (s512)"
+            s512["int8_ffn"] = {"value": round(B * steps2 / dt28, 2),
+                                "ms_per_step": round(dt28 / steps2 * 1e3, 4)}
+            enc.disable_int8_ffn()
     del enc
     torch.cuda.empty_cache()
 
+    _log("E4 hybrid encoder")
     e4 = None if args.no_e4 else e4_hybrid(torch)
-    roof = measure_kernels(torch, dev, ["gemm_ffn_up"])[0]
-    kernels = None if args.no_kernels else measure_kernels(torch, dev)
+    _log("kernel table")
+    kernels = measure_kernels(torch, dev, None if not args.no_kernels else STEP_KERNELS)
+    # the roofline line is the step's dominant kernel: the longest of the
+    # kernels one encoder layer launches, as measured just now
+    roof = max((k for k in kernels if k["name"] in STEP_KERNELS), key=lambda k: k["us"])
+    _log("CPU baseline")
     cpu = None if args.no_cpu else cpu_baseline(S, args.layers, args.cpu_seconds)
     fwd_flops = args.layers * (2 * B * S * 768 * (3 * 768 + 768 + 2 * 3072) + 4 * B * 12 * S * S * 64)
     line = {
@@ -486,11 +634,14 @@ def main():
         "encoder_tflops": round(fwd_flops * args.steps / dt / 1e12, 2),
         "int8_ffn": int8,
         "encoder_s512": s512,
-        "roofline": {"bound": "mfma", "achieved": roof["achieved"], "peak": roof["peak"],
-                     "unit": roof["unit"], "frac": roof["frac"], "traffic": pmc_traffic()},
-        "roofline_kernel": {"kernel": "gemm_mfma_kernel<F16, bias+gelu_erf> M=4096 K=768 N=3072",
-                            "avg_launch_us": roof["us"], "flops_per_launch": 2.0 * 4096 * 768 * 3072},
-        "kernels": kernels,
+        "roofline": {"bound": roof["bound"], "achieved": roof["achieved"], "peak": roof["peak"],
+                     "unit": roof["unit"], "frac": roof["frac"],
+                     "traffic": pmc_traffic(roof["name"])},
+        "roofline_kernel": {"name": roof["name"], "kernel": KERNEL_DESC[roof["name"]],
+                            "avg_launch_us": roof["us"],
+                            "per_step_candidates_us": {k["name"]: k["us"] for k in kernels
+                                                       if k["name"] in STEP_KERNELS}},
+        "kernels": None if args.no_kernels else kernels,
         "e4_hybrid": e4,
         "cpu_baseline": cpu,
     }

@@ -90,6 +90,18 @@ int zk_layernorm(const void *x, const void *residual, const void *gamma,
                  const void *beta, void *y, int64_t rows, int64_t hidden,
                  float eps, int dtype, void *stream);
 
+/* y = LayerNorm(x) * gamma + beta + residual (the residual is added AFTER
+ * normalisation), same shapes, dtypes and statistics as zk_layernorm;
+ * residual must not be NULL. Replaces fused_layernorm_add
+ * (core/src/fused_kernels.cu:224-296, 401-407), the kernel of the GraphIR
+ * `LayerNormAdd` node that FusionPass emits for LayerNormalization -> Add
+ * (zenith/optimization/fusion_pass.py:295-303). The reference's single-pass
+ * variance E[x^2] - mean^2 (fused_kernels.cu:242-283) is replaced by exact
+ * two-pass statistics. */
+int zk_layernorm_add(const void *x, const void *residual, const void *gamma,
+                     const void *beta, void *y, int64_t rows, int64_t hidden,
+                     float eps, int dtype, void *stream);
+
 /* zk_layernorm (fp16) that also writes q = quant(y, q_scale) as int8
  * [rows, hidden] (quant as in zk_quantize_i8, applied to the fp16 output),
  * for an int8 GEMM that consumes the normalised rows. Equals zk_layernorm
@@ -134,7 +146,10 @@ int zk_gemm_f32(const float *A, const float *B, float *C, int64_t M,
  *   O[b,h,s,:] = softmax(scale * Q[b,h,s,:] . K[b,h,:,:]^T) . V[b,h,:,:]
  * Tensors are addressed by strides (elements): strides[0..2] are the
  * (batch, head, seq) strides of Q, [3..5] of K, [6..8] of V, [9..11] of O;
- * the head_dim axis is contiguous. head_dim in {64, 128}.
+ * the head_dim axis is contiguous. Any head_dim <= 128 (the reference's
+ * HEAD_DIM_MAX, flash_attention.cu:26); fp16 needs a multiple of 8. Kernels
+ * are compiled for widths 32, 64 and 128; other widths are zero-padded
+ * inside the kernel.
  * valid_lens (int32 [B], may be NULL): keys j >= valid_lens[b] are masked
  * (probability exactly 0); a row with no valid key yields 0.
  * dtype ZK_F16 (MFMA path) or ZK_F32 (fp32 path).

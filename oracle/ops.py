@@ -126,6 +126,18 @@ def add_layernorm(x: np.ndarray, residual: np.ndarray, gamma: np.ndarray, beta: 
     return layernorm(x.astype(F32) + residual.astype(F32), gamma, beta, eps)
 
 
+def layernorm_add(x: np.ndarray, residual: np.ndarray, gamma: np.ndarray, beta: np.ndarray,
+                  eps: float = 1e-5) -> np.ndarray:
+    """LayerNorm(x) * gamma + beta + residual, the residual added after the
+    normalisation (fused_layernorm_add_kernel, core/src/fused_kernels.cu:
+    224-296: statistics of x only, `normalized * gamma[i] + beta[i] +
+    res_row[i]` at :292). The reference's GPU kernel takes the single-pass
+    variance E[x^2] - mean^2 (:263); this restatement takes the two-pass
+    variance of `layernorm` (the two agree to fp32 rounding for
+    zero-mean-ish rows, and the two-pass form is the exact one)."""
+    return (layernorm(x, gamma, beta, eps) + residual.astype(F32)).astype(F32, copy=False)
+
+
 # ----------------------------------------------------------- attention -----
 
 

@@ -49,8 +49,27 @@ def test_library_exports_every_declared_symbol():
                                 L.ZK_I32, None), L.ZK_ERR_INVALID),  # int32 out + epilogue
     (lambda lib: lib.zk_gemm_i8(16, 16, 16, 8, 8, 16, 16, 16, 8, 1.0, None, None, None, 0, 0,
                                 L.ZK_F16, None), L.ZK_ERR_INVALID),  # dequant without s_w
-    (lambda lib: lib.zk_flash_attn_fwd(16, 16, 16, 16, 1, 1, 8, 8, 48, L.strides_arg([0] * 12),
+    (lambda lib: lib.zk_flash_attn_fwd(16, 16, 16, 16, 1, 1, 8, 8, 136, L.strides_arg([0] * 12),
                                        None, 0.125, L.ZK_F16, None), L.ZK_ERR_UNSUPPORTED),
+    (lambda lib: lib.zk_flash_attn_fwd(16, 16, 16, 16, 1, 1, 8, 8, 129, L.strides_arg([0] * 12),
+                                       None, 0.125, L.ZK_F32, None), L.ZK_ERR_UNSUPPORTED),
+    (lambda lib: lib.zk_flash_attn_fwd(16, 16, 16, 16, 1, 1, 8, 8, 20, L.strides_arg([0] * 12),
+                                       None, 0.125, L.ZK_F16, None),
+     L.ZK_ERR_UNSUPPORTED),  # fp16 head_dim not a multiple of 8
+    (lambda lib: lib.zk_gemm_f16(16, 16, 16, 8, 8, 8, 1 << 23, 8, 8, 1, L.ZK_F16, None, None, 0, 0,
+                                 None), L.ZK_ERR_UNSUPPORTED),  # A tile span beyond 31 bits
+    (lambda lib: lib.zk_gemm_f16(16, 16, 16, 8, 8, 8, 8, 1 << 23, 8, 1, L.ZK_F16, None, None, 0, 0,
+                                 None), L.ZK_ERR_UNSUPPORTED),  # W tile span beyond 31 bits
+    (lambda lib: lib.zk_gemm_i8(16, 16, 16, 8, 8, 131072, 131072, 131072, 8, 1.0, None, None, None,
+                                0, 0, L.ZK_I32, None), L.ZK_ERR_UNSUPPORTED),  # 128^2 K = 2^31
+    (lambda lib: lib.zk_gemm_i8(16, 16, 16, 8, 8, 16, 1 << 24, 16, 8, 1.0, None, None, None, 0, 0,
+                                L.ZK_I32, None), L.ZK_ERR_UNSUPPORTED),  # int8 span
+    (lambda lib: lib.zk_gemm_i8_requant(16, 16, 16, 8, 8, 16, 16, 1 << 24, 8, 1.0, 16, None, 0,
+                                        1.0, None), L.ZK_ERR_UNSUPPORTED),  # int8 span (W)
+    (lambda lib: lib.zk_layernorm_add(16, None, 16, 16, 16, 4, 8, 1e-5, L.ZK_F32, None),
+     L.ZK_ERR_INVALID),  # LayerNormAdd needs its residual
+    (lambda lib: lib.zk_layernorm_add(16, 16, 16, 16, 16, 4, 8, 1e-5, L.ZK_I8, None),
+     L.ZK_ERR_UNSUPPORTED),
     (lambda lib: lib.zk_flash_attn_fwd(16, 16, 16, 16, 1, 1, 8, 8, 64, L.strides_arg([0] * 12),
                                        None, -1.0, L.ZK_F16, None), L.ZK_ERR_INVALID),
     (lambda lib: lib.zk_quantize_i8(16, 16, 4, 0.0, L.ZK_F32, None), L.ZK_ERR_INVALID),

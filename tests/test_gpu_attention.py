@@ -54,15 +54,68 @@ def test_flash_attention_f16(dev, B, H, S, D, masked):
 
 @pytest.mark.parametrize("S", [128, 512])
 def test_flash_attention_config3(dev, S):
-    """Config 3: B=32, H=12, D=64, lengths ~ U{S/2..S}; checked on 4 sequences
-    (batch entries are independent)."""
+    """Config 3: B=32, H=12, D=64, lengths ~ U{S/2..S}; every one of the 32
+    sequences against the float64 oracle."""
     B, H, D = 32, 12, 64
     q, k, v = _qkv(B, H, S, S, D, tag=10)
     lens = synthetic.padding_lengths(B, S)
     o = _run(dev, q, k, v, lens, torch.float16)
-    pick = [0, 7, 19, 31]
-    ok, worst = fp16_tol(o[pick], ops.attention(q[pick], k[pick], v[pick], lens[pick]))
+    for lo in range(0, B, 8):
+        sl = slice(lo, lo + 8)
+        ok, worst = fp16_tol(o[sl], ops.attention(q[sl], k[sl], v[sl], lens[sl]))
+        assert ok, (lo, worst)
+
+
+@pytest.mark.parametrize("S", [128, 512])
+def test_flash_attention_config3_batch_invariance(dev, S):
+    """Each of the 32 sequences run alone (B=1, where the workgroup remap of
+    B*H % 8 == 0 grids is off) is bit-identical to its row of the B=32
+    launch: the arithmetic of a (batch, head) does not depend on where its
+    workgroups land, so any batch-indexing error shows as a mismatch."""
+    from zenith_amd import zenith_cuda as zc
+
+    B, H, D = 32, 12, 64
+    q, k, v = (torch.from_numpy(a).to(dev, torch.float16) for a in _qkv(B, H, S, S, D, tag=10))
+    lens = torch.from_numpy(synthetic.padding_lengths(B, S)).to(dev)
+    full = zc.flash_attention(q, k, v, key_padding_lengths=lens)
+    for b in range(B):
+        one = zc.flash_attention(q[b:b + 1], k[b:b + 1], v[b:b + 1],
+                                 key_padding_lengths=lens[b:b + 1])
+        assert torch.equal(one, full[b:b + 1]), b
+
+
+@pytest.mark.parametrize("D", [8, 24, 40, 48, 56, 72, 80, 96, 112, 120])
+@pytest.mark.parametrize("S", [77, 128, 300])
+def test_flash_attention_f16_any_head_dim(dev, D, S):
+    """head_dim below the compiled widths 32 / 64 / 128 (zero-padded inside
+    the kernel), masked, ragged lengths."""
+    B, H = 3, 2
+    q, k, v = _qkv(B, H, S, S, D, tag=100 + D)
+    lens = np.array([S, S // 2 + 1, 1], np.int32)
+    o = _run(dev, q, k, v, lens, torch.float16)
+    assert o.shape == (B, H, S, D)
+    ok, worst = fp16_tol(o, ops.attention(q, k, v, lens))
     assert ok, worst
+
+
+@pytest.mark.parametrize("D", [5, 20, 33, 100])
+def test_flash_attention_f16_odd_head_dim(dev, D):
+    """fp16 head_dims that are not a multiple of 8: padded to one by the
+    Python layer, scale still 1/sqrt(D)."""
+    q, k, v = _qkv(2, 3, 70, 70, D, tag=120 + D)
+    lens = np.array([70, 40], np.int32)
+    o = _run(dev, q, k, v, lens, torch.float16)
+    assert o.shape == (2, 3, 70, D)
+    ok, worst = fp16_tol(o, ops.attention(q, k, v, lens))
+    assert ok, worst
+
+
+@pytest.mark.parametrize("D", [1, 17, 48, 80, 96, 127])
+def test_flash_attention_f32_any_head_dim(dev, D):
+    q, k, v = _qkv(2, 2, 65, 65, D, f16=False, tag=140 + D)
+    lens = np.array([65, 33], np.int32)
+    o = _run(dev, q, k, v, lens, torch.float32)
+    np.testing.assert_allclose(o, ops.attention(q, k, v, lens), rtol=1e-4, atol=1e-5)
 
 
 def test_flash_attention_edge_lengths(dev):

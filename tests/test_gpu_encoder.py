@@ -36,8 +36,9 @@ def test_config1_single_layer(dev):
 
 @pytest.mark.parametrize("S", [128, 512])
 def test_config5_encoder_fp16(dev, S):
-    """12 layers, B=32, lengths ~ U{S/2..S}; the oracle runs on 2 of the 32
-    sequences (sequences are independent through the encoder)."""
+    """12 layers, B=32, lengths ~ U{S/2..S}, against the fp32 oracle: every
+    sequence at S=128; at S=512 eight sequences spread over the batch (the
+    full batch is covered bit-exactly by the permutation test below)."""
     from zenith_amd.encoder import BertEncoder
 
     B = 32
@@ -47,18 +48,45 @@ def test_config5_encoder_fp16(dev, S):
     enc = BertEncoder(w, device=dev)
     y = enc(torch.from_numpy(x).to(dev, torch.float16), torch.from_numpy(lens).to(dev)).float().cpu().numpy()
     assert np.isfinite(y).all()
-    pick = [0, 17]
+    pick = np.arange(B) if S == 128 else np.array([0, 5, 9, 14, 18, 23, 27, 31])
     rel = _check(y[pick], obert.bert_encoder(x[pick], w, lens[pick]))
-    rel16 = _check(y[pick], obert.bert_encoder(x[pick], w, lens[pick], act_f16=True))
-    print(f"encoder S={S}: rel vs fp32 oracle {rel:.3e}, vs fp16-storage oracle {rel16:.3e}")
+    two = pick[[0, -1]]
+    rel16 = _check(y[two], obert.bert_encoder(x[two], w, lens[two], act_f16=True))
+    print(f"encoder S={S}: rel vs fp32 oracle {rel:.3e} ({len(pick)} sequences), "
+          f"vs fp16-storage oracle {rel16:.3e}")
 
 
-def test_config5_encoder_int8_ffn(dev):
-    """INT8-FFN variant at B=32 S=128: scales calibrated on the GPU fp16 run,
-    the oracle's INT8 encoder uses the same scales and weight quantisation."""
+@pytest.mark.parametrize("S,int8", [(128, False), (512, False), (128, True), (512, True)])
+def test_config5_batch_permutation_invariance(dev, S, int8):
+    """The B=32 batch run in reversed order gives every sequence's output
+    bit-identical to the forward order: each output row depends only on its
+    own sequence, through kernels whose K-reduction order does not depend on
+    where a row or a (batch, head) lands in the grid. A batch-indexing error
+    (a wrong length, head or row offset for some batch entries) breaks it."""
     from zenith_amd.encoder import BertEncoder
 
-    B, S = 32, 128
+    B = 32
+    w = _r16(synthetic.bert_weights(12, seed=42))
+    x = synthetic.round_f16(synthetic.hidden_states(B, S, seed=42))
+    lens = synthetic.padding_lengths(B, S)
+    enc = BertEncoder(w, device=dev)
+    if int8:
+        enc.enable_int8_ffn([4.5 / 127] * 12, [6.0 / 127] * 12, layers_fp32=w)
+    perm = np.arange(B)[::-1].copy()
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    y = enc(T(x).half(), T(lens))
+    yp = enc(T(x[perm]).half(), T(lens[perm]))
+    assert torch.equal(yp, y[torch.from_numpy(perm).to(dev)])
+
+
+@pytest.mark.parametrize("S", [128, 512])
+def test_config5_encoder_int8_ffn(dev, S):
+    """INT8-FFN variant at B=32, S=128 and S=512: per-layer activation scales
+    calibrated on the oracle's fp32 activations; the oracle's INT8 encoder
+    uses the same scales and weight quantisation."""
+    from zenith_amd.encoder import BertEncoder
+
+    B = 32
     w = _r16(synthetic.bert_weights(12, seed=42))
     x = synthetic.round_f16(synthetic.hidden_states(B, S, seed=42))
     lens = synthetic.padding_lengths(B, S)
@@ -98,20 +126,22 @@ def test_config5_encoder_int8_ffn(dev):
         ref_i = obert.bert_layer(h, lw, lens[pick], int8=int8_layers[i], act_f16=True)
         y_i = enc.forward_layers(torch.from_numpy(h).to(dev, torch.float16), lp, i, i + 1)
         rel_i = _check(y_i.float().cpu().numpy(), ref_i)
-        print(f"int8 layer {i}: rel {rel_i:.3e}")
+        print(f"int8 S={S} layer {i}: rel {rel_i:.3e}")
         h = synthetic.round_f16(ref_i)
-    # End to end over 12 layers, a quantisation-boundary flip (one int8 step
-    # of an activation whose fp16 value differs in the last bit between the
-    # two implementations) turns a ~1e-3 difference into a full int8 step for
-    # that element, and such flips compound through the remaining layers; the
-    # 12-layer INT8 bar is therefore norm-relative 5e-2 without an elementwise
-    # bound (the fp16 encoder keeps both at 2e-2; each INT8 layer above holds
-    # 2e-2 elementwise).
+    # End to end over 12 layers at the encoder bar, norm-relative 2e-2. An
+    # activation whose fp16 value differs in the last bit between the two
+    # implementations can land on the other side of an int8 rounding boundary
+    # (a full quantisation step for that element) and such flips propagate
+    # through the remaining layers, so the elementwise excess is reported,
+    # not asserted, for the chain (each layer above holds it).
     ref = obert.bert_encoder(x[pick], w, lens[pick], int8_layers=int8_layers, act_f16=True)
-    rel = _check(y[pick], ref, bar=5e-2, elementwise=False)
+    rel = float(np.linalg.norm(y[pick] - ref) / np.linalg.norm(ref))
+    worst = float(np.max(np.abs(y[pick] - ref) - (2e-2 + 2e-2 * np.abs(ref))))
     ref16 = obert.bert_encoder(x[pick], w, lens[pick])
     rel16 = float(np.linalg.norm(y[pick] - ref16) / np.linalg.norm(ref16))
-    print(f"int8 encoder: rel vs int8 oracle {rel:.3e}, vs fp32 model {rel16:.3e}")
+    print(f"int8 encoder S={S}: rel vs int8 oracle {rel:.3e} (elementwise excess {worst:.3e}), "
+          f"vs fp32 model {rel16:.3e}")
+    assert rel <= 2e-2, (rel, worst)
     assert rel16 < 0.1
 
 

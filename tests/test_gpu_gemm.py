@@ -155,6 +155,30 @@ def test_matmul_fp32_strided_b(dev):
                                    rtol=1e-5, atol=1e-4)
 
 
+@pytest.mark.parametrize("M,K,N", [(256, 512, 384), (9, 10, 11), (64, 3, 33)])
+def test_matmul_broadcast_operands(dev, M, K, N):
+    """Broadcast views (expand(): stride(0) == 0) hold one row in memory; the
+    product must read that row for every output row, never M rows of it (a
+    past-the-allocation read). fp32 (transpose + MFMA route and SIMT route)
+    and fp16 wmma_matmul."""
+    from zenith_amd import zenith_cuda as zc
+
+    x = synthetic.uniform((1, K), tag=15)
+    y = synthetic.uniform((1, N), tag=16)
+    ref = ops.matmul_f64(np.broadcast_to(x, (M, K)), np.broadcast_to(y, (K, N)))
+    ta = _t(x, dev, torch.float32).expand(M, K)
+    tb = _t(y, dev, torch.float32).expand(K, N)
+    assert ta.stride(0) == 0 and tb.stride(0) == 0
+    c = zc.matmul(ta, tb)
+    np.testing.assert_allclose(c.cpu().numpy(), ref, rtol=1e-5, atol=1e-4)
+    x16, y16 = synthetic.round_f16(x), synthetic.round_f16(y)
+    c16 = zc.wmma_matmul(_t(x16, dev, torch.float16).expand(M, K),
+                         _t(y16, dev, torch.float16).expand(K, N))
+    ok, worst = fp16_tol(c16.cpu().numpy(), ops.matmul_f64(np.broadcast_to(x16, (M, K)),
+                                                           np.broadcast_to(y16, (K, N))))
+    assert ok, worst
+
+
 @pytest.mark.parametrize("M,K,N", [
     (4100, 72, 4100),   # 8-wave 256x256 tile
     (4000, 100, 2000),  # 8-wave 256x192 tile

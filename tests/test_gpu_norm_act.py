@@ -50,6 +50,55 @@ def test_layernorm(dev, rows, hidden, dtype, with_res):
         assert ok, worst
 
 
+@pytest.mark.parametrize("rows,hidden", [(1, 768), (4096, 768), (33, 1024), (7, 100),
+                                         (16, 8192)])
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_layernorm_add(dev, rows, hidden, dtype):
+    """LayerNormAdd: LN(x) * g + b + residual (the residual after the
+    normalisation); hidden=100 takes the block-per-row kernel."""
+    from zenith_amd import zenith_cuda as zc
+
+    x = synthetic.normal((rows, hidden), tag=51) * 3 + 0.5
+    r = synthetic.normal((rows, hidden), tag=52)
+    g = synthetic.normal((hidden,), tag=53, std=0.5) + 1
+    b = synthetic.normal((hidden,), tag=54, std=0.1)
+    eps = 1e-12 if hidden == 768 else 1e-5
+    tdt = torch.float32 if dtype == "f32" else torch.float16
+    if dtype == "f16":
+        x, r, g, b = (synthetic.round_f16(a) for a in (x, r, g, b))
+    y = zc.layernorm_add(_t(x, dev, tdt), _t(r, dev, tdt), _t(g, dev, tdt), _t(b, dev, tdt), eps)
+    y = y.float().cpu().numpy()
+    ref = ops.layernorm_add(x, r, g, b, eps)
+    if dtype == "f32":
+        np.testing.assert_allclose(y, ref, rtol=1e-5, atol=1e-5)
+    else:
+        ok, worst = fp16_tol(y, ref)
+        assert ok, worst
+
+
+def test_layernorm_add_through_the_registry(dev):
+    """The GraphIR LayerNormAdd node, dispatched through the registry to the
+    HIP kernel, in both node forms."""
+    from zenith_amd.hooks.dispatcher import ExecutionContext, KernelDispatcher, Node
+    from zenith_amd.hooks.kernel_registry import KernelRegistry, Precision
+
+    reg = KernelRegistry()
+    reg.initialize()
+    d = KernelDispatcher(registry=reg, precision=Precision.FP16)
+    x = synthetic.round_f16(synthetic.normal((64, 768), tag=55))
+    r = synthetic.round_f16(synthetic.normal((64, 768), tag=56))
+    g = synthetic.round_f16(synthetic.normal((768,), tag=57, std=0.3) + 1)
+    b = synthetic.round_f16(synthetic.normal((768,), tag=58, std=0.1))
+    T = lambda a: _t(a, dev, torch.float16)  # noqa: E731
+    ctx = ExecutionContext({"x": T(x), "r": T(r), "g": T(g), "b": T(b)})
+    y1 = d.dispatch(Node("LayerNormAdd", ["x", "r"], ["o"], {"epsilon": 1e-12}), ctx,
+                    {"weight": T(g), "bias": T(b)})
+    y2 = d.dispatch(Node("LayerNormAdd", ["x", "g", "b", "r"], ["o2"], {"epsilon": 1e-12}), ctx)
+    assert torch.equal(y1, y2)
+    ok, worst = fp16_tol(y1.float().cpu().numpy(), ops.layernorm_add(x, r, g, b, 1e-12))
+    assert ok, worst
+
+
 def test_layernorm_default_eps_and_unit_stats(dev):
     """layernorm(input, gamma, beta) uses eps=1e-5 like the reference
     binding; with gamma=1, beta=0 rows have mean 0 / std 1."""

@@ -181,6 +181,74 @@ def test_hip_registry_needs_the_library(tmp_path, monkeypatch):
         k = reg.get_kernel(op, Precision.FP16)
         assert k is not None and k.priority == 25 and k.name.startswith("hip_"), op
     assert reg.get_kernel("Linear", Precision.INT8).name.startswith("hip_qlinear")
+    assert reg.get_kernel("LayerNormAdd", Precision.FP32).name.startswith("hip_layernorm_add")
+
+
+_FUSED_OPS = ("Linear", "Gemm", "MatMul", "LayerNorm", "FusedAddLayerNorm", "AddLayerNorm",
+              "LayerNormAdd", "FusedBiasGeLU", "LinearGelu", "QKVProjection", "FlashAttention",
+              "Attention", "FusedAttentionEpilogue", "FusedFFN", "Gelu", "Relu")
+
+
+def test_binding_into_a_foreign_registry():
+    """register_hip_kernels on a registry whose Precision is a different Enum
+    class (as the reference's is): get_kernel must find the HIP specs at
+    FP32, FP16 and INT8, fused op types included. Before the specs were built
+    from the registry's own types, every lookup here returned None."""
+    from tests import _stand_in_registry as ref
+    from zenith_amd.hooks.kernels import register_hip_kernels
+
+    assert ref.Precision is not Precision and ref.Precision.FP16 != Precision.FP16
+    reg = ref.KernelRegistry()
+    assert register_hip_kernels(reg) > 0
+    for prec in (ref.Precision.FP32, ref.Precision.FP16):
+        for op in _FUSED_OPS:
+            k = reg.get_kernel(op, prec)
+            assert k is not None and k.name.startswith("hip_"), (op, prec)
+            assert isinstance(k, ref.KernelSpec) and k.precision is prec and k.priority == 25
+    k8 = reg.get_kernel("Linear", ref.Precision.INT8)
+    assert k8.name.startswith("hip_qlinear") and k8.precision is ref.Precision.INT8
+    # BF16 has no HIP spec: the reference rule falls back to FP32
+    assert reg.get_kernel("Linear", ref.Precision.BF16).precision is ref.Precision.FP32
+
+
+def test_binding_with_explicit_types():
+    """Explicit spec_cls / precision_enum win over the registry's module; a
+    precision the enum lacks is skipped."""
+    import enum
+    from tests import _stand_in_registry as ref
+    from zenith_amd.hooks.kernels import register_hip_kernels
+
+    P2 = enum.Enum("P2", {"FP32": "fp32", "FP16": "fp16"})
+    reg = ref.KernelRegistry()
+    register_hip_kernels(reg, spec_cls=ref.KernelSpec, precision_enum=P2)
+    assert reg.get_kernel("Linear", P2.FP16).precision is P2.FP16
+    assert not any(k.name.startswith("hip_qlinear") for k in reg._kernels["Linear"])
+
+
+def test_register_backend_replaces_an_existing_name():
+    """The reference's `import zenith` registers "zenith" first; ours must
+    take the name over (or refuse loudly), never keep the other one."""
+    from torch._dynamo.backends import registry as R
+
+    name = "zenith_amd_test_backend"
+
+    def other(gm, example_inputs):
+        return gm.forward
+
+    R._COMPILER_FNS.pop(name, None)
+    R._BACKENDS.pop(name, None)
+    R.register_backend(compiler_fn=other, name=name)
+    try:
+        with pytest.raises(RuntimeError):
+            backend.register_backend(name=name, replace=False)
+        assert R.lookup_backend(name) is other
+        ours = backend.register_backend(name=name)
+        assert R.lookup_backend(name) is ours and ours is not other
+        ours2 = backend.register_backend(name=name)  # again: replaces our own
+        assert R.lookup_backend(name) is ours2
+    finally:
+        R._COMPILER_FNS.pop(name, None)
+        R._BACKENDS.pop(name, None)
 
 
 # ---------------------------------------------------------- dispatcher ----
@@ -198,7 +266,8 @@ class _Rec:
 def _disp(rec, prec=Precision.FP32):
     reg = KernelRegistry()
     for op in ("Linear", "MatMul", "LayerNorm", "FusedAddLayerNorm", "GELU", "FusedBiasGeLU",
-               "Attention", "FlashAttention", "QKVProjection", "FusedFFN", "LinearGelu"):
+               "Attention", "FlashAttention", "QKVProjection", "FusedFFN", "LinearGelu",
+               "LayerNormAdd"):
         reg.register(_spec(op, [op], prec, 25, fn=rec(op)))
     return KernelDispatcher(registry=reg, precision=prec)
 
@@ -237,6 +306,24 @@ def test_dispatcher_fused_ops_and_eps():
     assert rec.calls[0][1][3] == 1e-12 and rec.calls[1][1][4] == 1e-5
     assert rec.calls[2][1][1] == "none"
     assert rec.calls[3][2] == {"key_padding_lengths": ctx.get_tensor("lens"), "scale": 0.125}
+
+
+def test_dispatcher_layernorm_add_marshalling():
+    """LayerNormAdd reaches fn(x, residual, gamma, beta, eps) from both node
+    forms: (x, residual) + affine weights, and the four LayerNormalization ->
+    Add inputs (x, scale, B, residual)."""
+    rec = _Rec()
+    d = _disp(rec)
+    x, r, g, b = (torch.full((2, 4), float(i)) for i in range(4))
+    ctx = ExecutionContext({"x": x, "r": r, "g": g[0], "b": b[0]})
+    d.dispatch(Node("LayerNormAdd", ["x", "r"], ["o"], {"epsilon": 1e-12}), ctx,
+               {"weight": g[0], "bias": b[0]})
+    d.dispatch(Node("FusedLayerNormAdd", ["x", "g", "b", "r"], ["o"]), ctx)
+    for name, args, _ in rec.calls:
+        assert name == "LayerNormAdd"
+        assert args[0] is x and args[1] is r
+        assert torch.equal(args[2], g[0]) and torch.equal(args[3], b[0])
+    assert rec.calls[0][1][4] == 1e-12 and rec.calls[1][1][4] == 1e-5
 
 
 def test_dispatcher_unsupported():

@@ -103,6 +103,26 @@ def test_add_layernorm_vs_reference_build():
                                    mod.fused.add_layernorm(x, r, g, b, eps), rtol=1e-4, atol=1e-5)
 
 
+@pytest.mark.parametrize("eps", [1e-12, 1e-5])
+def test_layernorm_add_vs_torch(eps):
+    """LN(x) * g + b + r: torch's F.layer_norm plus the residual; with unit
+    affine the residual-free part has unit-normal rows; and it differs from
+    the pre-add LN(x + r) (a swapped residual placement fails here)."""
+    x = synthetic.normal((64, 768), tag=15) * 2 + 0.5
+    r = synthetic.normal((64, 768), tag=16)
+    g = synthetic.normal((768,), tag=17) + 1
+    b = synthetic.normal((768,), tag=18)
+    t = (F.layer_norm(torch.from_numpy(x), (768,), torch.from_numpy(g), torch.from_numpy(b), eps)
+         + torch.from_numpy(r)).numpy()
+    y = ops.layernorm_add(x, r, g, b, eps)
+    np.testing.assert_allclose(y, t, rtol=1e-4, atol=1e-5)
+    one, zero = np.ones(768, np.float32), np.zeros(768, np.float32)
+    y1 = ops.layernorm_add(x, r, one, zero, eps) - r
+    np.testing.assert_allclose(y1.mean(-1), 0, atol=1e-5)
+    np.testing.assert_allclose(y1.std(-1), 1, atol=1e-4)
+    assert np.abs(y - ops.add_layernorm(x, r, g, b, eps)).max() > 0.5
+
+
 # ------------------------------------------------------------------ GELU ---
 def test_sigmoid_tanh_closed_forms():
     """sigmoid(0) = 1/2, sigmoid(x) + sigmoid(-x) = 1, saturation at +-inf,

@@ -44,6 +44,7 @@ SIGNATURES: dict[str, list] = {
     "zk_gelu": [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp],
     "zk_layernorm": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp],
     "zk_layernorm_q8": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _f32, _vp],
+    "zk_layernorm_add": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp],
     "zk_transpose_f16": [_vp, _vp, _i64, _i64, _i64, _i64, _vp],
     "zk_gemm_f16": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
                     _vp, _vp, _i64, _i32, _vp],

@@ -29,6 +29,7 @@ struct AttnParams {
   const void *Q, *K, *V;
   void *O;
   int B, H, Sq, Sk;
+  int D;  // head_dim as stored; kernels compiled for a wider width zero-pad to it
   int64_t sq[3], sk[3], sv[3], so[3];  // (batch, head, seq) strides
   const int32_t *valid_lens;
   float scale_log2;  // softmax scale * log2(e)
@@ -87,7 +88,10 @@ __device__ __forceinline__ int kv_swz16(int r) {
   return 2 * (((r >> 1) & 3) ^ ((r >> 2) & 2)) + ((r >> 3) & 1);
 }
 
-template <int D, int NW>
+// PAD: the stored head_dim p.D (a multiple of 8) is below the compiled D;
+// dims >= p.D of Q, K and V are read as zeros (they add nothing to Q.K^T and
+// produce output columns that are not stored).
+template <int D, int NW, bool PAD = false>
 __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
   constexpr int KT = 64;
   constexpr int NT = NW * 64;
@@ -113,8 +117,9 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
   f16x8 qf[D / 16];
 #pragma unroll
   for (int c = 0; c < D / 16; ++c)
-    qf[c] = qvalid ? *(const f16x8 *)(Qb + qrow * p.sq[2] + c * 16 + h32 * 8)
-                   : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    qf[c] = qvalid && (!PAD || c * 16 + h32 * 8 < p.D)
+                ? *(const f16x8 *)(Qb + qrow * p.sq[2] + c * 16 + h32 * 8)
+                : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
 
   f32x16 o[D / 32];
 #pragma unroll
@@ -130,11 +135,12 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
     for (int v = 0; v < PER; ++v) {
       const int idx = tid + v * NT;
       const int kk = t * KT + idx / DV;  // K: 16-byte vectors row-contiguous
-      kr[v] = kk < p.Sk ? *(const f16x8 *)(Kb + kk * p.sk[2] + (idx % DV) * 8)
-                        : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      const bool in = kk < p.Sk && (!PAD || (idx % DV) * 8 < p.D);
+      kr[v] = in ? *(const f16x8 *)(Kb + kk * p.sk[2] + (idx % DV) * 8)
+                 : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
       // V like K (8 lanes per 128-byte row, coalesced)
-      vr[v] = kk < p.Sk ? *(const f16x8 *)(Vb + kk * p.sv[2] + (idx % DV) * 8)
-                        : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      vr[v] = in ? *(const f16x8 *)(Vb + kk * p.sv[2] + (idx % DV) * 8)
+                 : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
     }
   };
   auto stash_kv = [&]() {
@@ -246,6 +252,7 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
     for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
+        if (PAD && dt * 32 + 8 * g + 4 * h32 >= p.D) continue;
         f16x4 out;
 #pragma unroll
         for (int j = 0; j < 4; ++j) out[j] = (f16)(o[dt][4 * g + j] * inv);
@@ -409,6 +416,8 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_q16_kernel(AttnParams p) {
 }
 
 // ---------------------------------------------------------------- fp32 ----
+// Compiled for D in {32, 64, 128}; a stored head_dim p.D <= D is zero-padded
+// (dims >= p.D are read as zeros and not stored).
 template <int D>
 __global__ __launch_bounds__(256) void fa_fwd_f32_kernel(AttnParams p) {
   constexpr int TPQ = D / 32;  // lanes per query
@@ -430,7 +439,7 @@ __global__ __launch_bounds__(256) void fa_fwd_f32_kernel(AttnParams p) {
   float q[32], acc[32];
 #pragma unroll
   for (int i = 0; i < 32; ++i) {
-    q[i] = qvalid ? Qb[qrow * p.sq[2] + part * 32 + i] : 0.f;
+    q[i] = qvalid && part * 32 + i < p.D ? Qb[qrow * p.sq[2] + part * 32 + i] : 0.f;
     acc[i] = 0.f;
   }
   float m = -__builtin_inff(), l = 0.f;
@@ -439,8 +448,9 @@ __global__ __launch_bounds__(256) void fa_fwd_f32_kernel(AttnParams p) {
     __syncthreads();
     for (int idx = tid; idx < KT * D; idx += 256) {
       const int kk = idx / D, d = idx % D, key = t * KT + kk;
-      Ks[kk][d] = key < p.Sk ? Kb[key * p.sk[2] + d] : 0.f;
-      Vs[kk][d] = key < p.Sk ? Vb[key * p.sv[2] + d] : 0.f;
+      const bool in = key < p.Sk && d < p.D;
+      Ks[kk][d] = in ? Kb[key * p.sk[2] + d] : 0.f;
+      Vs[kk][d] = in ? Vb[key * p.sv[2] + d] : 0.f;
     }
     __syncthreads();
     float s[KT];
@@ -472,11 +482,12 @@ __global__ __launch_bounds__(256) void fa_fwd_f32_kernel(AttnParams p) {
   if (qvalid) {
     const float inv = l > 0.f ? 1.0f / l : 0.f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) Ob[qrow * p.so[2] + part * 32 + i] = acc[i] * inv;
+    for (int i = 0; i < 32; ++i)
+      if (part * 32 + i < p.D) Ob[qrow * p.so[2] + part * 32 + i] = acc[i] * inv;
   }
 }
 
-template <int D>
+template <int D, bool PAD = false>
 static void launch_f16(const AttnParams &p, hipStream_t s) {
   // 4 wavefronts x 32 queries per workgroup: at seq 128 one workgroup holds a
   // whole (batch, head), so K and V are read from HBM once.
@@ -484,7 +495,7 @@ static void launch_f16(const AttnParams &p, hipStream_t s) {
   // workgroup. The shorter per-wave chain and the doubled wave count win
   // where the kernel is latency-bound (encoder 0.5% faster per step at b32
   // s128); at s512 the 32-query kernel's lower LDS traffic per query wins.
-  if constexpr (D == 64) {
+  if constexpr (D == 64 && !PAD) {
     if (p.Sq <= 128) {
       // one 64-key tile per LDS stage, the next one loading under the
       // current one's MFMAs. Staging both tiles of a 128-key sequence at once
@@ -497,10 +508,10 @@ static void launch_f16(const AttnParams &p, hipStream_t s) {
   }
   if (p.Sq >= 128) {
     dim3 grid((unsigned)((p.Sq + 127) / 128), (unsigned)p.H, (unsigned)p.B);
-    fa_fwd_f16_kernel<D, 4><<<grid, 256, 0, s>>>(p);
+    fa_fwd_f16_kernel<D, 4, PAD><<<grid, 256, 0, s>>>(p);
   } else {
     dim3 grid((unsigned)((p.Sq + 63) / 64), (unsigned)p.H, (unsigned)p.B);
-    fa_fwd_f16_kernel<D, 2><<<grid, 128, 0, s>>>(p);
+    fa_fwd_f16_kernel<D, 2, PAD><<<grid, 128, 0, s>>>(p);
   }
 }
 
@@ -528,8 +539,9 @@ extern "C" int zk_flash_attn_fwd(const void *Q, const void *K, const void *V,
     return fail(ZK_ERR_INVALID, "zk_flash_attn_fwd: null pointer");
   if (batch > 65535 || heads > 65535 || seq_q > 0x7fffffff || seq_k > 0x7fffffff)
     return fail(ZK_ERR_UNSUPPORTED, "zk_flash_attn_fwd: size exceeds launch limits");
-  if (head_dim != 32 && head_dim != 64 && head_dim != 128)
-    return fail(ZK_ERR_UNSUPPORTED, "zk_flash_attn_fwd: head_dim %lld not in {32, 64, 128}",
+  // any head_dim up to 128, the reference's HEAD_DIM_MAX (flash_attention.cu:26)
+  if (head_dim > 128)
+    return fail(ZK_ERR_UNSUPPORTED, "zk_flash_attn_fwd: head_dim %lld > 128",
                 (long long)head_dim);
   if (!(scale > 0.0f) || scale == __builtin_inff())
     return fail(ZK_ERR_INVALID, "zk_flash_attn_fwd: scale must be finite and > 0");
@@ -538,6 +550,7 @@ extern "C" int zk_flash_attn_fwd(const void *Q, const void *K, const void *V,
   AttnParams p;
   p.Q = Q; p.K = K; p.V = V; p.O = O;
   p.B = (int)batch; p.H = (int)heads; p.Sq = (int)seq_q; p.Sk = (int)seq_k;
+  p.D = (int)head_dim;
   for (int i = 0; i < 3; ++i) {
     p.sq[i] = strides[i]; p.sk[i] = strides[3 + i];
     p.sv[i] = strides[6 + i]; p.so[i] = strides[9 + i];
@@ -551,12 +564,20 @@ extern "C" int zk_flash_attn_fwd(const void *Q, const void *K, const void *V,
         return fail(ZK_ERR_UNSUPPORTED, "zk_flash_attn_fwd: fp16 strides must be multiples of 8");
     if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O))
       return fail(ZK_ERR_UNSUPPORTED, "zk_flash_attn_fwd: fp16 tensors must be 16-byte aligned");
+    if (head_dim % 8)
+      return fail(ZK_ERR_UNSUPPORTED,
+                  "zk_flash_attn_fwd: fp16 head_dim must be a multiple of 8 (got %lld)",
+                  (long long)head_dim);
+    // compiled widths 32 / 64 / 128; narrower head_dims are zero-padded
     if (head_dim == 32) launch_f16<32>(p, s);
     else if (head_dim == 64) launch_f16<64>(p, s);
-    else launch_f16<128>(p, s);
+    else if (head_dim == 128) launch_f16<128>(p, s);
+    else if (head_dim < 32) launch_f16<32, true>(p, s);
+    else if (head_dim < 64) launch_f16<64, true>(p, s);
+    else launch_f16<128, true>(p, s);
   } else if (dtype == ZK_F32) {
-    if (head_dim == 32) launch_f32<32>(p, s);
-    else if (head_dim == 64) launch_f32<64>(p, s);
+    if (head_dim <= 32) launch_f32<32>(p, s);
+    else if (head_dim <= 64) launch_f32<64>(p, s);
     else launch_f32<128>(p, s);
   } else {
     return fail(ZK_ERR_UNSUPPORTED, "zk_flash_attn_fwd: dtype %d not supported", dtype);

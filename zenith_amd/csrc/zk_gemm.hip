@@ -726,6 +726,18 @@ static int check_dims(const char *who, int64_t M, int64_t N, int64_t K) {
   return ZK_OK;
 }
 
+// The MFMA kernel addresses a tile's rows through a buffer descriptor of
+// (rows - 1) * ld + K bytes (rows <= 256) with 32-bit offsets, and pushes
+// K-tail chunks out of range with the offset 0x7ffffff0; both operands'
+// spans must stay below it.
+static int check_span(const char *who, int64_t lda, int64_t ldb, int64_t K, int elem) {
+  const int64_t lim = 0x7ffffff0LL;
+  if (255 * lda * elem + K * elem >= lim || 255 * ldb * elem + K * elem >= lim)
+    return fail(ZK_ERR_UNSUPPORTED,
+                "%s: leading dimension / K too large for 32-bit tile addressing", who);
+  return ZK_OK;
+}
+
 }  // namespace zk
 
 using namespace zk;
@@ -756,6 +768,7 @@ static int gemm_f16_impl(const void *A, const void *B, void *C, int64_t M, int64
   if (out_dtype != ZK_F16 && out_dtype != ZK_F32)
     return fail(ZK_ERR_UNSUPPORTED, "zk_gemm_f16: out_dtype %d not supported", out_dtype);
   if (K == 0) return fail(ZK_ERR_UNSUPPORTED, "zk_gemm_f16: K == 0");
+  if ((st = check_span("zk_gemm_f16", lda, ldb, K, 2))) return st;
   GemmParams p{A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc, bias, residual, ldr, 1.f, nullptr, 0};
   hipStream_t s = as_stream(stream);
   const SplitPlan sp = plan_split(M, N, K, 2);
@@ -804,9 +817,10 @@ static int check_i8(const char *who, const int8_t *A, const int8_t *W, const voi
     return fail(ZK_ERR_UNSUPPORTED,
                 "%s: K, lda, ldw must be multiples of 16 and A, W 16-byte aligned", who);
   if (K == 0) return fail(ZK_ERR_UNSUPPORTED, "%s: K == 0", who);
-  if (K > 131072)
-    return fail(ZK_ERR_UNSUPPORTED, "%s: K > 131072 could overflow int32 accumulators", who);
-  return ZK_OK;
+  // |acc| <= 128 * 128 * K, which reaches 2^31 (int32 overflow) at K = 131072
+  if (K >= 131072)
+    return fail(ZK_ERR_UNSUPPORTED, "%s: K >= 131072 could overflow int32 accumulators", who);
+  return check_span(who, lda, ldw, K, 1);
 }
 
 extern "C" int zk_gemm_i8(const int8_t *A, const int8_t *W, void *C, int64_t M,
@@ -889,7 +903,7 @@ static int gemm_f32_impl(const float *A, const float *B, float *C, int64_t M, in
   // products, fp32 accumulation); buffer offsets of a 256-row tile must fit
   // in 31 bits.
   if (trans_b && K > 0 && K % 4 == 0 && lda % 4 == 0 && ldb % 4 == 0 && aligned16(A) &&
-      aligned16(B) && lda < (1 << 21) && ldb < (1 << 21)) {
+      aligned16(B) && 255 * (lda + ldb) * 4 + 2 * K * 4 < 0x7ffffff0LL) {
     GemmParams p{A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc, bias, res, ldr, 1.f, nullptr, 0};
     const SplitPlan sp = plan_split(M, N, K, 4);
     if (ws && sp.splits > 1 && ws_bytes >= split_ws_bytes(M, N, sp) && aligned16(ws))

@@ -1,4 +1,5 @@
-// LayerNorm and fused Add+LayerNorm (post-LN BERT residual), fp32 statistics.
+// LayerNorm, fused Add+LayerNorm (post-LN BERT residual: LN(x + r)) and
+// LayerNorm+Add (LN(x) + r, the reference's LayerNormAdd), fp32 statistics.
 //
 // Fast path: one or two rows per wavefront. Each lane keeps its slice of the
 // row in registers as 16-byte vectors, so the row is read from HBM exactly once
@@ -17,11 +18,15 @@ template <> struct LnVec<float> { typedef f32x4 type; static constexpr int n = 4
 
 constexpr int kLnWaves = 4;  // wavefronts per 256-thread block
 
+// Residual placement: none, added before the statistics (Add+LayerNorm), or
+// added to the normalised output (LayerNorm+Add).
+enum { kResNone = 0, kResPre = 1, kResPost = 2 };
+
 // LPR lanes per row (64 / LPR rows per wavefront): a 768-wide fp16 row is 96
 // 16-byte vectors, so two rows per wavefront give every lane exactly three.
 // Q8: also write q = quant(y) as int8 (the fp16 output value quantised with
 // scale qs), for an int8 GEMM that consumes the normalised rows.
-template <typename T, int MAXV, bool RES, int LPR, bool Q8>
+template <typename T, int MAXV, int RES, int LPR, bool Q8>
 __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
     const T *__restrict__ x, const T *__restrict__ res,
     const T *__restrict__ gamma, const T *__restrict__ beta, T *__restrict__ y,
@@ -37,7 +42,7 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
   const bool live = row < rows;
   const int nvec = hidden / W;
   const V *xr = reinterpret_cast<const V *>(x + (live ? row : 0) * hidden);
-  const V *rr = reinterpret_cast<const V *>(res + (RES && live ? row * hidden : 0));
+  const V *rr = reinterpret_cast<const V *>(res + (RES != kResNone && live ? row * hidden : 0));
 
   float v[MAXV][W];
   float sum = 0.f;
@@ -47,11 +52,11 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
     if (live && idx < nvec) {
       V a = xr[idx];
       V r;
-      if (RES) r = rr[idx];
+      if (RES == kResPre) r = rr[idx];
 #pragma unroll
       for (int j = 0; j < W; ++j) {
         float f = (float)a[j];
-        if (RES) f += (float)r[j];
+        if (RES == kResPre) f += (float)r[j];
         v[k][j] = f;
         sum += f;
       }
@@ -90,9 +95,16 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
     const int idx = sub + k * LPR;
     if (idx < nvec) {
       V g = gv[idx], b = bv[idx], o;
+      if constexpr (RES == kResPost) {
+        const V r = rr[idx];
 #pragma unroll
-      for (int j = 0; j < W; ++j)
-        o[j] = (T)((v[k][j] - mean) * rstd * (float)g[j] + (float)b[j]);
+        for (int j = 0; j < W; ++j)
+          o[j] = (T)((v[k][j] - mean) * rstd * (float)g[j] + (float)b[j] + (float)r[j]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < W; ++j)
+          o[j] = (T)((v[k][j] - mean) * rstd * (float)g[j] + (float)b[j]);
+      }
       store_nt(yr + idx, o);
       if constexpr (Q8) {
         static_assert(W == 8, "int8 output is written 8 bytes per vector");
@@ -110,7 +122,7 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
 }
 
 // Generic fallback: one 256-thread block per row, three passes over the row.
-template <typename T, bool RES, bool Q8>
+template <typename T, int RES, bool Q8>
 __global__ __launch_bounds__(256) void ln_block_kernel(
     const T *__restrict__ x, const T *__restrict__ res,
     const T *__restrict__ gamma, const T *__restrict__ beta, T *__restrict__ y,
@@ -118,7 +130,8 @@ __global__ __launch_bounds__(256) void ln_block_kernel(
   __shared__ float part[256 / kWave];
   const int64_t row = blockIdx.x;
   const T *xr = x + row * hidden;
-  const T *rr = RES ? res + row * hidden : nullptr;
+  const T *rr = RES != kResNone ? res + row * hidden : nullptr;
+  constexpr bool PRE = RES == kResPre;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid >> 6;
   constexpr int NW = 256 / kWave;
 
@@ -135,17 +148,19 @@ __global__ __launch_bounds__(256) void ln_block_kernel(
 
   float s = 0.f;
   for (int64_t i = tid; i < hidden; i += 256)
-    s += (float)xr[i] + (RES ? (float)rr[i] : 0.f);
+    s += (float)xr[i] + (PRE ? (float)rr[i] : 0.f);
   const float mean = block_sum(s) / (float)hidden;
   float sq = 0.f;
   for (int64_t i = tid; i < hidden; i += 256) {
-    const float d = (float)xr[i] + (RES ? (float)rr[i] : 0.f) - mean;
+    const float d = (float)xr[i] + (PRE ? (float)rr[i] : 0.f) - mean;
     sq += d * d;
   }
   const float rstd = 1.0f / sqrtf(block_sum(sq) / (float)hidden + eps);
   for (int64_t i = tid; i < hidden; i += 256) {
-    const float f = (float)xr[i] + (RES ? (float)rr[i] : 0.f);
-    const T o = (T)((f - mean) * rstd * (float)gamma[i] + (float)beta[i]);
+    const float f = (float)xr[i] + (PRE ? (float)rr[i] : 0.f);
+    float yv = (f - mean) * rstd * (float)gamma[i] + (float)beta[i];
+    if (RES == kResPost) yv += (float)rr[i];
+    const T o = (T)yv;
     y[row * hidden + i] = o;
     if (Q8) q[row * hidden + i] = quant1((float)o, qs, 1.0f / qs);
   }
@@ -153,21 +168,29 @@ __global__ __launch_bounds__(256) void ln_block_kernel(
 
 template <typename T, int MAXV, int LPR, bool Q8>
 static void ln_wave_launch(const T *x, const T *r, const T *g, const T *b, T *y, int8_t *q,
-                           float qs, int64_t rows, int hidden, float eps, hipStream_t s) {
+                           float qs, int64_t rows, int hidden, float eps, bool post,
+                           hipStream_t s) {
   constexpr int rows_per_block = kLnWaves * (kWave / LPR);
   const unsigned grid = (unsigned)((rows + rows_per_block - 1) / rows_per_block);
-  if (r)
-    ln_wave_kernel<T, MAXV, true, LPR, Q8><<<grid, kLnWaves * kWave, 0, s>>>(
+  if (r && post) {
+    if constexpr (!Q8)
+      ln_wave_kernel<T, MAXV, kResPost, LPR, false><<<grid, kLnWaves * kWave, 0, s>>>(
+          x, r, g, b, y, q, qs, rows, hidden, eps);
+  } else if (r) {
+    ln_wave_kernel<T, MAXV, kResPre, LPR, Q8><<<grid, kLnWaves * kWave, 0, s>>>(
         x, r, g, b, y, q, qs, rows, hidden, eps);
-  else
-    ln_wave_kernel<T, MAXV, false, LPR, Q8><<<grid, kLnWaves * kWave, 0, s>>>(
+  } else {
+    ln_wave_kernel<T, MAXV, kResNone, LPR, Q8><<<grid, kLnWaves * kWave, 0, s>>>(
         x, r, g, b, y, q, qs, rows, hidden, eps);
+  }
 }
 
+// post: the residual is added after normalisation (LN(x) + r) instead of
+// before it (LN(x + r)); never combined with the int8 output.
 template <typename T, bool Q8>
 static int ln_impl(const void *xv, const void *rv, const void *gv,
                    const void *bv, void *yv, int8_t *q, float qs, int64_t rows,
-                   int64_t hidden, float eps, hipStream_t s) {
+                   int64_t hidden, float eps, hipStream_t s, bool post = false) {
   const T *x = (const T *)xv, *r = (const T *)rv, *g = (const T *)gv,
           *b = (const T *)bv;
   T *y = (T *)yv;
@@ -180,7 +203,7 @@ static int ln_impl(const void *xv, const void *rv, const void *gv,
     const int h = (int)hidden;
     // 32 lanes per row while a row fits in 4 vectors per lane (H <= 1024 in
     // fp16), else a whole wavefront per row.
-#define ZK_LN(MV, LPR) ln_wave_launch<T, MV, LPR, Q8>(x, r, g, b, y, q, qs, rows, h, eps, s)
+#define ZK_LN(MV, LPR) ln_wave_launch<T, MV, LPR, Q8>(x, r, g, b, y, q, qs, rows, h, eps, post, s)
     if (nvec <= 32) ZK_LN(1, 32);
     else if (nvec <= 64) ZK_LN(2, 32);
     else if (nvec <= 96) ZK_LN(3, 32);
@@ -192,10 +215,15 @@ static int ln_impl(const void *xv, const void *rv, const void *gv,
   } else {
     if (rows > 0x7fffffff)
       return fail(ZK_ERR_UNSUPPORTED, "zk_layernorm: too many rows for the generic path");
-    if (r)
-      ln_block_kernel<T, true, Q8><<<(unsigned)rows, 256, 0, s>>>(x, r, g, b, y, q, qs, hidden, eps);
-    else
-      ln_block_kernel<T, false, Q8><<<(unsigned)rows, 256, 0, s>>>(x, r, g, b, y, q, qs, hidden, eps);
+    if (r && post) {
+      if constexpr (!Q8)
+        ln_block_kernel<T, kResPost, false><<<(unsigned)rows, 256, 0, s>>>(x, r, g, b, y, q, qs,
+                                                                          hidden, eps);
+    } else if (r) {
+      ln_block_kernel<T, kResPre, Q8><<<(unsigned)rows, 256, 0, s>>>(x, r, g, b, y, q, qs, hidden, eps);
+    } else {
+      ln_block_kernel<T, kResNone, Q8><<<(unsigned)rows, 256, 0, s>>>(x, r, g, b, y, q, qs, hidden, eps);
+    }
   }
   return check_launch("zk_layernorm");
 }
@@ -237,4 +265,20 @@ extern "C" int zk_layernorm_q8(const void *x, const void *residual, const void *
   if (!(q_scale > 0.f)) return fail(ZK_ERR_INVALID, "zk_layernorm_q8: q_scale must be > 0");
   return ln_impl<f16, true>(x, residual, gamma, beta, y, q, q_scale, rows, hidden, eps,
                             as_stream(stream));
+}
+
+extern "C" int zk_layernorm_add(const void *x, const void *residual, const void *gamma,
+                                const void *beta, void *y, int64_t rows, int64_t hidden,
+                                float eps, int dtype, void *stream) {
+  int st = ln_check("zk_layernorm_add", x, gamma, beta, y, rows, hidden, eps);
+  if (st || rows == 0) return st;
+  if (!residual) return fail(ZK_ERR_INVALID, "zk_layernorm_add: null residual");
+  hipStream_t s = as_stream(stream);
+  if (dtype == ZK_F32)
+    return ln_impl<float, false>(x, residual, gamma, beta, y, nullptr, 1.f, rows, hidden, eps, s,
+                                 true);
+  if (dtype == ZK_F16)
+    return ln_impl<f16, false>(x, residual, gamma, beta, y, nullptr, 1.f, rows, hidden, eps, s,
+                               true);
+  return fail(ZK_ERR_UNSUPPORTED, "zk_layernorm_add: dtype %d not supported", dtype);
 }

@@ -53,11 +53,23 @@ def create_compile_backend(target: str = "cuda", precision: str = "fp32",
     return zenith_backend
 
 
-def register_backend(name: str = "zenith", **kwargs) -> Callable:
-    """Register the backend with torch._dynamo under `name` (idempotent)."""
-    from torch._dynamo import list_backends, register_backend as _reg
+def register_backend(name: str = "zenith", replace: bool = True, **kwargs) -> Callable:
+    """Register the backend with torch._dynamo under `name` and return it.
+
+    The reference's `import zenith` already registers a backend called
+    "zenith" (zenith/integrations/torch_dynamo.py:158-170), and dynamo
+    refuses a second registration of a name. With replace=True (default) an
+    existing registration of `name` is removed first, so
+    torch.compile(backend="zenith") reaches these kernels; with replace=False
+    a taken name raises RuntimeError instead of being silently kept."""
+    from torch._dynamo.backends import registry as _r
 
     backend = create_compile_backend(**kwargs)
-    if name not in list_backends(exclude_tags=()):
-        _reg(compiler_fn=backend, name=name)
+    taken = name in _r._COMPILER_FNS or name in _r.list_backends(exclude_tags=())
+    if taken:
+        if not replace:
+            raise RuntimeError(f"a torch.compile backend named {name!r} is already registered")
+        _r._COMPILER_FNS.pop(name, None)
+        _r._BACKENDS.pop(name, None)
+    _r.register_backend(compiler_fn=backend, name=name)
     return backend

@@ -97,6 +97,7 @@ class KernelDispatcher:
         "BiasGeLU": "FusedBiasGeLU",
         "Bias+GELU": "FusedBiasGeLU",
         "FusedLinearGelu": "LinearGelu",
+        "FusedLayerNormAdd": "LayerNormAdd",
         "flash_attention": "FlashAttention",
     }
 
@@ -177,6 +178,14 @@ class KernelDispatcher:
         if op == "FusedAddLayerNorm":
             return fn(inputs[0], inputs[1], w(weights, "weight", "gamma"),
                       w(weights, "bias", "beta"), eps)
+        if op == "LayerNormAdd":
+            # LayerNormalization(x, scale, B) -> Add(., residual): either the
+            # four node inputs in that order, or (x, residual) with the affine
+            # parameters as weights
+            if len(inputs) >= 4:
+                return fn(inputs[0], inputs[3], inputs[1], inputs[2], eps)
+            return fn(inputs[0], inputs[1], w(weights, "weight", "gamma", "scale"),
+                      w(weights, "bias", "beta", "B"), eps)
         if op == "GELU":
             return fn(inputs[0], attrs.get("approximate", "tanh"))
         if op == "FusedBiasGeLU":

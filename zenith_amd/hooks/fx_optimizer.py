@@ -211,7 +211,7 @@ _LINEAR = {F.linear, torch._C._nn.linear}
 _GELU = {F.gelu, torch._C._nn.gelu}
 _LAYERNORM = {F.layer_norm, torch.layer_norm}
 _ADD = {operator.add, operator.iadd, torch.add}
-_HEAD_DIMS = (32, 64, 128)
+_MAX_HEAD_DIM = 128  # the kernel's limit (the reference's HEAD_DIM_MAX)
 
 
 def _arg(node, i, name, default=None):
@@ -288,7 +288,7 @@ def _as_sdpa(node):
     if float(_arg(node, 4, "dropout_p", 0.0) or 0.0) != 0.0 or node.kwargs.get("enable_gqa"):
         return None
     d = _meta_last_dim(q)
-    if d is not None and d not in _HEAD_DIMS:
+    if d is not None and d > _MAX_HEAD_DIM:
         return None
     return [q, k, v, node.kwargs.get("scale")]
 

@@ -5,6 +5,7 @@ type (what KernelDispatcher passes):
   MatMul                       fn(A[M,K], B[K,N])
   LayerNorm                    fn(x, gamma, beta, eps)
   FusedAddLayerNorm            fn(x, residual, gamma, beta, eps)
+  LayerNormAdd                 fn(x, residual, gamma, beta, eps)   LN(x) + residual
   Gelu / FusedBiasGeLU         fn(x) / fn(x, bias)          (approximate= kw)
   Relu                         fn(x)
   Attention / FlashAttention   fn(q, k, v, key_padding_lengths=None, scale=None)
@@ -18,6 +19,8 @@ another device raise RuntimeError (no fallback).
 """
 
 from __future__ import annotations
+
+import sys
 
 import torch
 
@@ -49,6 +52,11 @@ def layernorm(x, gamma, beta, eps: float = 1e-5):
 
 def add_layernorm(x, residual, gamma, beta, eps: float = 1e-5):
     return zc.add_layernorm(_rows(x), _rows(residual), gamma, beta, eps).view(x.shape)
+
+
+def layernorm_add(x, residual, gamma, beta, eps: float = 1e-5):
+    """LayerNorm(x) * gamma + beta + residual (the LayerNormAdd node)."""
+    return zc.layernorm_add(_rows(x), _rows(residual), gamma, beta, eps).view(x.shape)
 
 
 def gelu(x, approximate: str = "tanh"):
@@ -104,6 +112,8 @@ _TABLE = [
      (Precision.FP32, Precision.FP16), layernorm),
     ("hip_add_layernorm", ["FusedAddLayerNorm", "AddLayerNorm", "Add+LayerNorm"],
      (Precision.FP32, Precision.FP16), add_layernorm),
+    ("hip_layernorm_add", ["LayerNormAdd", "FusedLayerNormAdd"],
+     (Precision.FP32, Precision.FP16), layernorm_add),
     ("hip_gelu", ["Gelu", "GELU", "gelu"], (Precision.FP32, Precision.FP16), gelu),
     ("hip_bias_gelu", ["FusedBiasGeLU", "BiasGeLU", "Bias+GELU"],
      (Precision.FP32, Precision.FP16), bias_gelu),
@@ -118,14 +128,45 @@ _TABLE = [
 ]
 
 
-def register_hip_kernels(reg: KernelRegistry) -> None:
-    """Register every HIP kernel at priority 25. Raises RuntimeError if the
-    library cannot be loaded (there is no other tier)."""
+def _registry_types(reg, spec_cls, precision_enum):
+    """KernelSpec class and Precision enum to build the specs from: the
+    explicit arguments, else the ones defined beside the registry's class
+    (the reference keeps all three in zenith/runtime/kernel_registry.py), else
+    this package's own."""
+    mod = sys.modules.get(type(reg).__module__)
+    if spec_cls is None:
+        spec_cls = getattr(mod, "KernelSpec", None) or KernelSpec
+    if precision_enum is None:
+        precision_enum = getattr(mod, "Precision", None) or Precision
+    return spec_cls, precision_enum
+
+
+def register_hip_kernels(reg, spec_cls=None, precision_enum=None) -> int:
+    """Register every HIP kernel at priority 25 in `reg` and return the
+    number of specs registered. Raises RuntimeError if the library cannot be
+    loaded (there is no other tier).
+
+    `reg` may be this package's KernelRegistry or the reference's
+    (zenith/runtime/kernel_registry.py:92-153). Its get_kernel filters with
+    `spec.precision == precision` on its OWN Precision enum, and members of
+    two Enum classes never compare equal, so the specs are built from the
+    registry's own KernelSpec / Precision (found beside the registry's class,
+    or passed explicitly), with each precision matched by its `.value`
+    ("fp32", "fp16", "int8"). A precision the caller's enum lacks is
+    skipped."""
     from .. import _lib
 
     _lib.load()
+    spec_cls, prec_enum = _registry_types(reg, spec_cls, precision_enum)
+    by_value = {m.value: m for m in prec_enum}
+    n = 0
     for name, ops, precs, fn in _TABLE:
         for prec in precs:
-            reg.register(KernelSpec(name=f"{name}_{prec.value}", op_types=list(ops),
-                                    precision=prec, kernel_fn=fn, priority=HIP_PRIORITY,
-                                    requires_gpu=True))
+            target = by_value.get(prec.value)
+            if target is None:
+                continue
+            reg.register(spec_cls(name=f"{name}_{prec.value}", op_types=list(ops),
+                                  precision=target, kernel_fn=fn, priority=HIP_PRIORITY,
+                                  requires_gpu=True))
+            n += 1
+    return n

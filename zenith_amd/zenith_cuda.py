@@ -131,6 +131,32 @@ def add_layernorm(input: torch.Tensor, residual: torch.Tensor | None,
     return out
 
 
+def layernorm_add(input: torch.Tensor, residual: torch.Tensor, gamma: torch.Tensor,
+                  beta: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    """LayerNorm(input) * gamma + beta + residual, the residual added after
+    normalisation (fused_layernorm_add, core/src/fused_kernels.cu:224-296,
+    401-407; the kernel of the GraphIR `LayerNormAdd` node,
+    zenith/optimization/fusion_pass.py:295-303)."""
+    _need_cuda(input, residual, gamma, beta)
+    if input.dim() != 2:
+        raise RuntimeError("Input must be 2D [batch, hidden]")
+    if residual is None:
+        raise RuntimeError("layernorm_add needs a residual")
+    dt = _float_dtype(input, "layernorm_add")
+    rows, hidden = input.shape
+    for t, name in ((gamma, "gamma"), (beta, "beta")):
+        if t.dtype != input.dtype or t.numel() != hidden:
+            raise RuntimeError(f"{name} must be [hidden] with the input dtype")
+    if residual.shape != input.shape or residual.dtype != input.dtype:
+        raise RuntimeError("residual must match input shape and dtype")
+    x = input.contiguous()
+    r = residual.contiguous()
+    out = torch.empty_like(x)
+    L.call("zk_layernorm_add", _p(x), _p(r), _p(gamma.contiguous()), _p(beta.contiguous()),
+           _p(out), rows, hidden, float(eps), dt, _stream(x))
+    return out
+
+
 def add_layernorm_q8(input: torch.Tensor, residual: torch.Tensor | None,
                      gamma: torch.Tensor, beta: torch.Tensor, eps: float,
                      q_scale: float) -> tuple[torch.Tensor, torch.Tensor]:
@@ -205,8 +231,11 @@ def transpose_f16(x: torch.Tensor) -> torch.Tensor:
     if x.dim() != 2 or x.dtype != torch.float16 or x.stride(1) != 1:
         raise RuntimeError("transpose_f16 expects a row-major 2-D fp16 tensor")
     R, C = x.shape
+    if R > 1 and x.stride(0) < C:  # overlapping rows (e.g. a broadcast view)
+        x = x.contiguous()
     out = torch.empty((C, R), dtype=torch.float16, device=x.device)
-    L.call("zk_transpose_f16", _p(x), _p(out), R, C, x.stride(0), out.stride(0), _stream(x))
+    L.call("zk_transpose_f16", _p(x), _p(out), R, C, x.stride(0) if R > 1 else C,
+           out.stride(0), _stream(x))
     return out
 
 
@@ -227,8 +256,8 @@ def wmma_matmul(A: torch.Tensor, B: torch.Tensor,
         raise RuntimeError("Matrix dimensions must match")
     if out_dtype not in (torch.float32, torch.float16):
         raise RuntimeError("out_dtype must be torch.float32 or torch.float16")
-    A = A if A.stride(1) == 1 else A.contiguous()
-    Bc = B if B.stride(1) == 1 else B.contiguous()
+    A = _rows_dense(A)
+    Bc = _rows_dense(B)
     if A.shape[0] == 0 or B.shape[1] == 0:
         return torch.empty((A.shape[0], B.shape[1]), dtype=out_dtype, device=A.device)
     if A.shape[1] == 0:
@@ -251,9 +280,18 @@ def matmul(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
         return wmma_matmul(A, B, out_dtype=torch.float16)
     if A.dtype != torch.float32 or B.dtype != torch.float32:
         raise RuntimeError("matmul expects two float32 (or two float16) tensors")
-    A = A if A.stride(1) == 1 else A.contiguous()
-    B = B if B.stride(1) == 1 else B.contiguous()
-    return _gemm_f32_nn(A, B)
+    return _gemm_f32_nn(_rows_dense(A), _rows_dense(B))
+
+
+def _rows_dense(t: torch.Tensor) -> torch.Tensor:
+    """t itself when its rows can be addressed as row r at r * stride(0) with
+    unit column stride and non-overlapping rows (stride(0) >= row length, or a
+    single row); otherwise a contiguous copy. Broadcast views (expand(),
+    stride(0) == 0) and other overlapping layouts are copied."""
+    rows, cols = t.shape
+    if t.stride(1) == 1 and (rows <= 1 or t.stride(0) >= cols):
+        return t
+    return t.contiguous()
 
 
 # fp32 products of at least this many multiply-adds (and K % 4 == 0) transpose
@@ -270,7 +308,9 @@ def _gemm_f32_nn(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
     if M == 0 or N == 0:
         return C
     s = _stream(A)
-    lda, ldb = max(A.stride(0), K), max(B.stride(0), N)
+    # single-row operands may carry any stride(0); use the dense row length
+    lda = A.stride(0) if M > 1 else K
+    ldb = B.stride(0) if K > 1 else N
     if K % 4 == 0 and M * N * K >= _F32_MFMA_MIN_MACS:
         bt = torch.empty((N, K), dtype=torch.float32, device=A.device)
         if ldb == N:
@@ -368,7 +408,9 @@ def flash_attention(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor,
     """softmax(scale . Q K^T) V over [batch, heads, seq, head_dim] tensors,
     non-causal (reference flash_attention_forward, flash_attention.cu:327-340,
     scale 1/sqrt(head_dim)). `key_padding_lengths` (int, [batch]) masks keys
-    j >= length; a query with no valid key returns 0. fp32 and fp16."""
+    j >= length; a query with no valid key returns 0. fp32 and fp16; any
+    head_dim up to 128 (HEAD_DIM_MAX, flash_attention.cu:26); fp16 head_dims
+    that are not a multiple of 8 are zero-padded to one."""
     if not Q.is_cuda:
         raise RuntimeError("Q must be CUDA tensor")
     _need_cuda(Q, K, V, key_padding_lengths)
@@ -387,15 +429,27 @@ def flash_attention(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor,
     def lastdim(t):
         return t if t.stride(3) == 1 else t.contiguous()
 
-    Q, K, V = lastdim(Q), lastdim(K), lastdim(V)
-    O = torch.empty((B, H, Sq, D), dtype=Q.dtype, device=Q.device)
+    if D > 128:
+        raise RuntimeError(f"flash_attention: head_dim {D} > 128 is not supported")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
     lens = None
     if key_padding_lengths is not None:
         lens = key_padding_lengths.to(device=Q.device, dtype=torch.int32).contiguous()
         if lens.numel() != B:
             raise RuntimeError("key_padding_lengths must have one entry per batch")
-    if scale is None:
-        scale = 1.0 / math.sqrt(D)
+    if dt == L.ZK_F16 and D % 8:
+        # zero columns add nothing to Q.K^T; V's give output columns dropped below
+        Dp = (D + 7) // 8 * 8
+        pad = lambda t: torch.nn.functional.pad(t, (0, Dp - D))  # noqa: E731
+        O = torch.empty((B, H, Sq, Dp), dtype=Q.dtype, device=Q.device)
+        Qp, Kp, Vp = pad(Q), pad(K), pad(V)
+        _attn_call(Qp, Kp, Vp, O, B, H, Sq, Sk, Dp,
+                   [*Qp.stride()[:3], *Kp.stride()[:3], *Vp.stride()[:3], *O.stride()[:3]],
+                   lens, scale, dt)
+        return O[..., :D].contiguous()
+    Q, K, V = lastdim(Q), lastdim(K), lastdim(V)
+    O = torch.empty((B, H, Sq, D), dtype=Q.dtype, device=Q.device)
     return _attn_call(Q, K, V, O, B, H, Sq, Sk, D,
                       [*Q.stride()[:3], *K.stride()[:3], *V.stride()[:3], *O.stride()[:3]],
                       lens, scale, dt)
@@ -516,6 +570,6 @@ def int8_linear_q8(a_q: torch.Tensor, w_q: torch.Tensor, s_x: float, s_w: torch.
 
 __all__ = [
     "relu", "gelu", "layernorm", "matmul", "flash_attention", "wmma_matmul",
-    "add_layernorm", "add_layernorm_q8", "bias_gelu", "linear", "transpose_f16",
+    "add_layernorm", "layernorm_add", "add_layernorm_q8", "bias_gelu", "linear", "transpose_f16",
     "quantize_int8", "int8_matmul", "int8_linear", "int8_linear_q8",
 ]
