@@ -246,6 +246,20 @@ int zk_gemm_f16_ws(const void *A, const void *B, void *C, int64_t M, int64_t N,
                    int out_dtype, const void *bias, const void *residual, int64_t ldr,
                    int epilogue, void *workspace, int64_t ws_bytes, void *stream);
 
+/* zk_gemm_f16 that allocates nothing and takes no workspace: for callers
+ * that cannot allocate device memory (code under HIP-graph capture, tight
+ * serving loops, hosts that forbid allocation). No counterpart in the
+ * reference. Same arguments, checks and results as zk_gemm_f16_ws with a
+ * workspace of zk_gemm_workspace_size(M, N, K, ZK_F16) bytes: small-M
+ * products are split along K, their fp32 partials kept in a static 4 MiB
+ * device array (one per GPU, held until the process ends; the split plan
+ * never needs more, and a larger need is rejected with ZK_ERR_UNSUPPORTED).
+ * Calls that overlap in time on one GPU race on that array. */
+int zk_gemm_f16_noalloc(const void *A, const void *B, void *C, int64_t M, int64_t N,
+                        int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_b,
+                        int out_dtype, const void *bias, const void *residual, int64_t ldr,
+                        int epilogue, void *stream);
+
 /* zk_gemm_f32 with a caller workspace of ws_bytes (split-K on the fp32
  * MFMA path); with a null or too small workspace it is zk_gemm_f32. */
 int zk_gemm_f32_ws(const float *A, const float *B, float *C, int64_t M, int64_t N,

@@ -62,6 +62,8 @@ SIGNATURES: dict[str, list] = {
     "zk_gemm_f16_ws": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
                        _vp, _vp, _i64, _i32, _vp, _i64, _vp],
     "zk_gemm_f32_ws": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _vp, _i64, _vp],
+    "zk_gemm_f16_noalloc": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
+                            _vp, _vp, _i64, _i32, _vp],
     "zk_embedding": [_vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
     "zk_bert_embeddings": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                            _i64, _i64, _i64, _f32, _i32, _vp],

@@ -46,6 +46,14 @@ __host__ __device__ inline bool aligned8(const void *p) {
 }
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 
+// The fp16 GEMM behind zk_gemm_f16 / zk_gemm_f16_ws (zk_gemm.hip): with a
+// device workspace `ws` of at least zk_gemm_workspace_size bytes, small-M
+// products are split along K through it; with none they run unsplit.
+int gemm_f16_impl(const void *A, const void *B, void *C, int64_t M, int64_t N, int64_t K,
+                  int64_t lda, int64_t ldb, int64_t ldc, int trans_b, int out_dtype,
+                  const void *bias, const void *residual, int64_t ldr, int epilogue, void *ws,
+                  int64_t ws_bytes, void *stream);
+
 // Symmetric int8 quantisation of one value,
 //   q = clamp(round_half_even(RN(x / scale)), -128, 127)
 // (quantize_f32_to_int8_kernel, core/src/cuda_kernels.cu:926-927), with

@@ -742,10 +742,10 @@ static int check_span(const char *who, int64_t lda, int64_t ldb, int64_t K, int 
 
 using namespace zk;
 
-static int gemm_f16_impl(const void *A, const void *B, void *C, int64_t M, int64_t N,
-                         int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_b,
-                         int out_dtype, const void *bias, const void *residual, int64_t ldr,
-                         int epilogue, void *ws, int64_t ws_bytes, void *stream) {
+int zk::gemm_f16_impl(const void *A, const void *B, void *C, int64_t M, int64_t N, int64_t K,
+                      int64_t lda, int64_t ldb, int64_t ldc, int trans_b, int out_dtype,
+                      const void *bias, const void *residual, int64_t ldr, int epilogue,
+                      void *ws, int64_t ws_bytes, void *stream) {
   int st = check_dims("zk_gemm_f16", M, N, K);
   if (st) return st;
   if (M == 0 || N == 0) return ZK_OK;
