@@ -163,6 +163,24 @@ int zk_flash_attn_fwd(const void *Q, const void *K, const void *V, void *O,
                       const int32_t *valid_lens, float scale, int dtype,
                       void *stream);
 
+/* zk_flash_attn_fwd with a boolean attention mask on top of valid_lens
+ * (which may be NULL): mask[b, h, q, k] != 0 keeps key k for query q, 0
+ * gives it probability exactly 0; a query with no kept key yields 0.
+ * mask is uint8, one byte per key with keys contiguous; mask_strides[0..2]
+ * are its (batch, head, query) strides in bytes, multiples of 4 (0
+ * broadcasts), mask is 4-byte aligned, and every row holds seq_k rounded up
+ * to a multiple of 4 bytes (keys are read 4 at a time; bytes past seq_k are
+ * ignored). This is the boolean attn_mask of
+ * scaled_dot_product_attention, [B|1, H|1, Sq|1, Sk], which the reference's
+ * FX replacement hands to torch (zenith/optimization/fx_patterns.py:106-114),
+ * with the masked-attention rule of zenith/jax/primitives.py:302-310. */
+int zk_flash_attn_fwd_masked(const void *Q, const void *K, const void *V, void *O,
+                             int64_t batch, int64_t heads, int64_t seq_q, int64_t seq_k,
+                             int64_t head_dim, const int64_t *strides,
+                             const int32_t *valid_lens, const uint8_t *mask,
+                             const int64_t *mask_strides, float scale, int dtype,
+                             void *stream);
+
 /* Symmetric int8 quantisation, q = clamp(round_half_even(x / scale),
  * -128, 127), x in dtype ZK_F32 or ZK_F16 (n elements, contiguous).
  * Replaces quantize_f32_to_int8_kernel (cuda_kernels.cu:918-937; numpy form

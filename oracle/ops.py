@@ -143,12 +143,14 @@ def layernorm_add(x: np.ndarray, residual: np.ndarray, gamma: np.ndarray, beta: 
 
 def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray,
               valid_lens: np.ndarray | None = None, scale: float | None = None,
-              dtype=np.float64) -> np.ndarray:
+              dtype=np.float64, mask: np.ndarray | None = None) -> np.ndarray:
     """Dense softmax(scale . Q K^T) V over [B, H, S, D] (reference semantics:
     flash_attention_forward core/src/flash_attention.cu:194-340, scale
     1/sqrt(D) at :330). Key-padding rule of the masked attention primitive
     (zenith/jax/primitives.py:302-310): keys j >= valid_lens[b] get -inf
-    logits and probability exactly 0; an all-masked row yields 0.
+    logits and probability exactly 0; an all-masked row yields 0. `mask`
+    (bool, broadcastable to [B, H, Sq, Sk], True = attend) applies the same
+    rule per (query, key) on top of valid_lens.
     Computed in float64 by default."""
     q = q.astype(dtype)
     k = k.astype(dtype)
@@ -160,8 +162,10 @@ def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray,
     s = np.matmul(q, np.swapaxes(k, -1, -2)) * scale  # [B,H,Sq,Sk]
     if valid_lens is not None:
         lens = np.clip(np.asarray(valid_lens).astype(np.int64), 0, Sk)
-        mask = np.arange(Sk)[None, :] < lens[:, None]  # [B, Sk]
-        s = np.where(mask[:, None, None, :], s, -np.inf)
+        keep = np.arange(Sk)[None, :] < lens[:, None]  # [B, Sk]
+        s = np.where(keep[:, None, None, :], s, -np.inf)
+    if mask is not None:
+        s = np.where(np.asarray(mask, dtype=bool), s, -np.inf)
     with np.errstate(invalid="ignore"):
         m = np.max(s, axis=-1, keepdims=True)
         e = np.exp(s - m)

@@ -110,6 +110,78 @@ def test_flash_attention_f16_odd_head_dim(dev, D):
     assert ok, worst
 
 
+def _mask_case(kind, B, H, S, rng):
+    """Boolean masks (True = attend) in the broadcast forms SDPA accepts."""
+    if kind == "hf_padding":  # HF BERT's SDPA mask: [B, 1, S, S], rows equal
+        lens = rng.integers(1, S + 1, size=B)
+        keep = np.arange(S)[None, :] < lens[:, None]
+        return np.broadcast_to(keep[:, None, None, :], (B, 1, S, S)).copy()
+    if kind == "keys_only":  # [B, 1, 1, S], not a prefix
+        return rng.random((B, 1, 1, S)) < 0.7
+    if kind == "per_query":  # [B, H, S, S] with some rows fully masked
+        m = rng.random((B, H, S, S)) < 0.5
+        m[0, 0, :3, :] = False
+        m[-1, -1, -1, :] = False
+        return m
+    if kind == "shared_2d":  # [S, S], broadcast over batch and heads
+        return rng.random((S, S)) < 0.8
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("B,H,S,D", [(2, 3, 128, 64), (2, 2, 300, 64), (2, 2, 77, 48),
+                                     (1, 2, 130, 128), (2, 2, 64, 32)])
+@pytest.mark.parametrize("kind", ["hf_padding", "keys_only", "per_query", "shared_2d"])
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_flash_attention_bool_mask(dev, B, H, S, D, kind, dtype):
+    """Boolean attn_mask on the 16-query kernel (S <= 128, D = 64), the
+    32-query kernel, the zero-padded head_dim kernel and fp32, combined with
+    key-padding lengths; rows with no key left give 0. S = 77 / 130 take the
+    padded mask copy (keys not a multiple of 4)."""
+    from zenith_amd import zenith_cuda as zc
+
+    kinds = ["hf_padding", "keys_only", "per_query", "shared_2d"]
+    rng = np.random.default_rng([B, H, S, D, kinds.index(kind)])
+    q, k, v = _qkv(B, H, S, S, D, f16=dtype == "f16", tag=160)
+    mask = _mask_case(kind, B, H, S, rng)
+    lens = np.full(B, S, np.int32)
+    lens[0] = max(1, S - 20)
+    tdt = torch.float16 if dtype == "f16" else torch.float32
+    t = [torch.from_numpy(a).to(dev, tdt) for a in (q, k, v)]
+    o = zc.flash_attention(*t, key_padding_lengths=torch.from_numpy(lens).to(dev),
+                           attn_mask=torch.from_numpy(mask).to(dev)).float().cpu().numpy()
+    ref = ops.attention(q, k, v, lens, mask=mask)
+    if dtype == "f16":
+        ok, worst = fp16_tol(o, ref)
+        assert ok, worst
+    else:
+        np.testing.assert_allclose(o, ref, rtol=1e-4, atol=1e-5)
+    empty = ~np.broadcast_to(mask, (B, H, S, S)).any(-1)
+    assert not o[empty].any()
+
+
+def test_flash_attention_mask_matches_lengths(dev):
+    """A prefix mask equal to the key-padding lengths gives the same output
+    as the lengths alone, bit for bit (config 3 at s128 and a 32-query
+    shape)."""
+    from zenith_amd import zenith_cuda as zc
+
+    for B, H, S in ((32, 12, 128), (4, 12, 512)):
+        q, k, v = (torch.from_numpy(a).to(dev, torch.float16) for a in _qkv(B, H, S, S, 64, tag=170))
+        lens = torch.from_numpy(synthetic.padding_lengths(B, S)).to(dev)
+        keep = torch.arange(S, device=dev)[None, :] < lens[:, None]
+        a = zc.flash_attention(q, k, v, key_padding_lengths=lens)
+        b = zc.flash_attention(q, k, v, attn_mask=keep[:, None, None, :])
+        assert torch.equal(a, b)
+
+
+def test_flash_attention_mask_rejects_float_masks(dev):
+    from zenith_amd import zenith_cuda as zc
+
+    q = torch.zeros(1, 1, 8, 64, device=dev, dtype=torch.float16)
+    with pytest.raises(RuntimeError):
+        zc.flash_attention(q, q, q, attn_mask=torch.zeros(8, 8, device=dev))
+
+
 @pytest.mark.parametrize("D", [1, 17, 48, 80, 96, 127])
 def test_flash_attention_f32_any_head_dim(dev, D):
     q, k, v = _qkv(2, 2, 65, 65, D, f16=False, tag=140 + D)

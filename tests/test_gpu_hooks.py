@@ -67,6 +67,32 @@ def test_torch_compile_backend(dev):
     _check(y, obert.bert_layer(x, w))
 
 
+def test_torch_compile_backend_padding_mask(dev):
+    """A padded batch: the boolean [B, 1, S, S] mask HF BERT's SDPA path
+    builds reaches the masked HIP attention kernel through torch.compile
+    (no SDPA left in the graph), and the layer matches the oracle layer with
+    the same key-padding lengths."""
+    import torch._dynamo
+
+    from zenith_amd.hooks import backend
+    from zenith_amd.torch_bert import MaskedTorchBertLayer
+
+    _, w, x, xt = _layer(dev)
+    m = MaskedTorchBertLayer(w).to(dev).half().eval()
+    B, S = x.shape[:2]
+    lens = np.array([S, S // 2 + 5], np.int32)
+    keep = torch.arange(S, device=dev)[None, :] < torch.from_numpy(lens).to(dev)[:, None]
+    mask = keep[:, None, None, :].expand(B, 1, S, S)
+    torch._dynamo.reset()
+    be = backend.create_compile_backend(precision="fp16")
+    cm = torch.compile(m, backend=be, dynamic=False)
+    with torch.no_grad():
+        y = cm(xt, mask).float().cpu().numpy()
+    st = be.last_stats
+    assert st is not None and "structural_sdpa_to_flash" in st.passes_applied, st
+    _check(y, obert.bert_layer(x, w, lens))
+
+
 def test_dispatcher_fused_ops(dev):
     from zenith_amd.hooks import ExecutionContext, KernelDispatcher, Node, Precision
 

@@ -330,3 +330,36 @@ def test_dispatcher_unsupported():
     d = _disp(_Rec())
     with pytest.raises(UnsupportedOperationError):
         d.dispatch(Node("Conv", ["a"], ["o"]), ExecutionContext({"a": torch.zeros(1)}))
+
+
+# ------------------------------------------------------ masked attention ----
+class _MaskedSDPA(torch.nn.Module):
+    def forward(self, q, k, v, mask):
+        return F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+
+
+@pytest.mark.parametrize("mask_dtype,rewritten", [(torch.bool, True), (torch.float32, False)])
+def test_sdpa_with_mask_rewrites_only_boolean_masks(mask_dtype, rewritten):
+    """With shape metadata on the graph (as torch.compile graphs carry), an
+    SDPA call with a boolean mask becomes the masked HIP attention leaf, the
+    mask passed through; an additive float mask stays with torch."""
+    from torch.fx.passes.shape_prop import ShapeProp
+
+    gm = torch.fx.symbolic_trace(_MaskedSDPA())
+    q = torch.randn(2, 3, 8, 16)
+    mask = torch.ones(2, 1, 8, 8, dtype=mask_dtype)
+    ShapeProp(gm).propagate(q, q, q, mask)
+    opt = O.FXOptimizer(require_gpu_inputs=False)
+    gm = opt.optimize(gm, [q, q, q, mask])
+    calls = [n for n in gm.graph.nodes if n.op == "call_function"]
+    hip = [n for n in calls if n.target is P.hip_attention]
+    assert bool(hip) == rewritten
+    if rewritten:
+        assert hip[0].args[4].op == "placeholder" and hip[0].args[4].name == "mask"
+        assert not any(n.target is F.scaled_dot_product_attention for n in calls)
+
+
+def test_sdpa_mask_of_unknown_dtype_is_left_alone():
+    gm = torch.fx.symbolic_trace(_MaskedSDPA())  # no shape metadata
+    gm = O.FXOptimizer(require_gpu_inputs=False).optimize(gm, [])
+    assert not any(n.op == "call_function" and n.target is P.hip_attention for n in gm.graph.nodes)

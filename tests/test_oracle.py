@@ -174,6 +174,29 @@ def test_attention_vs_torch_sdpa_masked():
         *(torch.from_numpy(a).double() for a in (q, k, v))).numpy(), rtol=1e-10, atol=1e-12)
 
 
+def test_attention_general_mask_vs_torch_sdpa():
+    """A boolean mask per (query, key) with rows that mask everything:
+    torch SDPA's boolean attn_mask where at least one key is kept, and
+    exactly 0 (the masked-primitive rule) for rows with none kept; a mask
+    equal to the valid-length prefix matches valid_lens."""
+    B, H, S, D = 2, 3, 24, 16
+    q, k, v = (synthetic.normal((B, H, S, D), tag=t) for t in (24, 25, 26))
+    rng = np.random.default_rng(5)
+    mask = rng.random((B, 1, S, S)) < 0.6
+    mask[0, 0, 3, :] = False  # a query with no key left
+    o = ops.attention(q, k, v, mask=mask)
+    t = F.scaled_dot_product_attention(*(torch.from_numpy(a).double() for a in (q, k, v)),
+                                       attn_mask=torch.from_numpy(mask)).numpy()
+    rows = mask.any(-1)  # [B,1,S]
+    keep = np.broadcast_to(rows[..., None], o.shape)
+    np.testing.assert_allclose(o[keep], t[keep], rtol=1e-10, atol=1e-12)
+    assert not o[0, :, 3].any()
+    lens = np.array([24, 9])
+    prefix = (np.arange(S)[None, :] < lens[:, None])[:, None, None, :]
+    np.testing.assert_allclose(ops.attention(q, k, v, mask=prefix), ops.attention(q, k, v, lens),
+                               rtol=0, atol=0)
+
+
 def test_attention_closed_forms():
     B, H, S, D = 2, 2, 16, 8
     q, k, v = (synthetic.normal((B, H, S, D), tag=t) for t in (21, 22, 23))

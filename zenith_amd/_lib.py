@@ -53,6 +53,9 @@ SIGNATURES: dict[str, list] = {
                       _vp, _i64, _vp],
     "zk_flash_attn_fwd": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                           ctypes.POINTER(_i64), _vp, _f32, _i32, _vp],
+    "zk_flash_attn_fwd_masked": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                 ctypes.POINTER(_i64), _vp, _vp, ctypes.POINTER(_i64), _f32,
+                                 _i32, _vp],
     "zk_quantize_i8": [_vp, _vp, _i64, _f32, _i32, _vp],
     "zk_gemm_i8": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _vp,
                    _vp, _vp, _i64, _i32, _i32, _vp],

@@ -32,8 +32,22 @@ struct AttnParams {
   int D;  // head_dim as stored; kernels compiled for a wider width zero-pad to it
   int64_t sq[3], sk[3], sv[3], so[3];  // (batch, head, seq) strides
   const int32_t *valid_lens;
+  // Optional boolean mask, one byte per (batch, head, query, key), nonzero =
+  // attend; (batch, head, query) strides in bytes (0 broadcasts), keys
+  // contiguous, every row 4-byte aligned (read 4 keys at a time).
+  const uint8_t *mask;
+  int64_t sm[3];
   float scale_log2;  // softmax scale * log2(e)
 };
+
+// The mask row of (b, h, q), and the 4 mask bytes of keys k0 .. k0 + 3 as one
+// word (k0 a multiple of 4; keys >= Sk read as masked).
+__device__ __forceinline__ const uint8_t *mask_row(const AttnParams &p, int b, int h, int q) {
+  return p.mask + b * p.sm[0] + h * p.sm[1] + (int64_t)q * p.sm[2];
+}
+__device__ __forceinline__ uint32_t mask4(const AttnParams &p, const uint8_t *row, int k0) {
+  return k0 < p.Sk ? *(const uint32_t *)(row + k0) : 0u;
+}
 
 __device__ __forceinline__ int valid_len(const AttnParams &p, int b) {
   if (!p.valid_lens) return p.Sk;
@@ -91,7 +105,10 @@ __device__ __forceinline__ int kv_swz16(int r) {
 // PAD: the stored head_dim p.D (a multiple of 8) is below the compiled D;
 // dims >= p.D of Q, K and V are read as zeros (they add nothing to Q.K^T and
 // produce output columns that are not stored).
-template <int D, int NW, bool PAD = false>
+// MASK: p.mask is applied on top of the valid lengths. A tile can then be
+// fully masked for a query that has seen no valid key yet (running max still
+// -inf); the rescale factor and the exponent are guarded for that case.
+template <int D, int NW, bool PAD = false, bool MASK = false>
 __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
   constexpr int KT = 64;
   constexpr int NT = NW * 64;
@@ -114,6 +131,7 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
 
   const int qrow = tile.qb * (NW * 32) + wave * 32 + (lane & 31);
   const bool qvalid = qrow < p.Sq;
+  const uint8_t *mrow = MASK ? mask_row(p, b, h, qvalid ? qrow : 0) : nullptr;
   f16x8 qf[D / 16];
 #pragma unroll
   for (int c = 0; c < D / 16; ++c)
@@ -185,19 +203,33 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
           if (key >= L) s[kb][r] = -__builtin_inff();
         }
     }
+    if constexpr (MASK) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const uint32_t m4 = mask4(p, mrow, t * KT + kb * 32 + 8 * g4 + 4 * h32);
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (((m4 >> (8 * j)) & 0xffu) == 0) s[kb][4 * g4 + j] = -__builtin_inff();
+        }
+    }
     float tmax = -__builtin_inff();
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; r += 2) tmax = fmaxf(tmax, fmaxf(s[kb][r], s[kb][r + 1]));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * p.scale_log2;  // finite: key t*KT < L
+    // finite unless MASK (without a mask, key t*KT < L is valid)
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * p.scale_log2;
     // Lazy rescaling: the reference point m (log2 units) only moves when the
     // tile max exceeds it by more than 8, so exp2(s - m) <= 256 always fits
     // fp16 and the accumulator is rescaled on a few tiles only. O / l is
     // independent of the reference point, so this is exact.
     if (__builtin_amdgcn_ballot_w64(tmax > m + 8.0f) != 0) {
       const float m_new = fmaxf(m, tmax);
-      const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 on the first tile
+      // 0 on the first tile; a query with no valid key yet keeps m = -inf
+      const float alpha = MASK && m_new == -__builtin_inff() ? 1.0f
+                                                             : __builtin_amdgcn_exp2f(m - m_new);
       m = m_new;
       l *= alpha;
 #pragma unroll
@@ -205,13 +237,15 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
     }
+    // with m = -inf every score of this query is -inf so far: exp2 gives 0
+    const float mneg = MASK && m == -__builtin_inff() ? 0.0f : -m;
     float psum = 0.f;
     f16x8 pf[2][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float e = __builtin_amdgcn_exp2f(fmaf(s[kb][r], p.scale_log2, -m));
+        const float e = __builtin_amdgcn_exp2f(fmaf(s[kb][r], p.scale_log2, mneg));
         psum += e;
         pf[kb][r >> 3][r & 7] = (f16)e;
       }
@@ -271,7 +305,7 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
 // 4 g + j for j < 4 and 16 + 4 g + (j - 4) otherwise, so the B operand is the
 // lane's own probabilities of key blocks 2 st and 2 st + 1, and the V^T
 // operand comes from two transposing reads 16 keys apart.
-template <int NW, int TPS = 1>
+template <int NW, int TPS = 1, bool MASK = false>
 __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_q16_kernel(AttnParams p) {
   constexpr int D = 64, KT = 64, NT = NW * 64, DV = D / 8;
   constexpr int PER = TPS * KT * DV / NT;  // TPS key tiles per LDS stage
@@ -291,6 +325,7 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_q16_kernel(AttnParams p) {
 
   const int qrow = tile.qb * (NW * 16) + wave * 16 + c16;
   const bool qvalid = qrow < p.Sq;
+  const uint8_t *mrow = MASK ? mask_row(p, b, h, qvalid ? qrow : 0) : nullptr;
   f16x8 qf[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks)
@@ -361,15 +396,26 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_q16_kernel(AttnParams p) {
           for (int r = 0; r < 4; ++r)
             if (t * KT + 16 * kb + 4 * g + r >= L) s4[kb][r] = -__builtin_inff();
       }
+      if constexpr (MASK) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          const uint32_t m4 = mask4(p, mrow, t * KT + 16 * kb + 4 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (((m4 >> (8 * r)) & 0xffu) == 0) s4[kb][r] = -__builtin_inff();
+        }
+      }
       float tmax = -__builtin_inff();
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
         tmax = fmaxf(tmax, fmaxf(fmaxf(s4[kb][0], s4[kb][1]), fmaxf(s4[kb][2], s4[kb][3])));
       tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * p.scale_log2;  // finite: key t*KT < L
+      // finite unless MASK (without a mask, key t*KT < L is valid)
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * p.scale_log2;
       if (__builtin_amdgcn_ballot_w64(tmax > m + 8.0f) != 0) {
         const float m_new = fmaxf(m, tmax);
-        const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+        const float alpha = MASK && m_new == -__builtin_inff() ? 1.0f
+                                                               : __builtin_amdgcn_exp2f(m - m_new);
         m = m_new;
         l *= alpha;
 #pragma unroll
@@ -377,13 +423,14 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_q16_kernel(AttnParams p) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) o[db][r] *= alpha;
       }
+      const float mneg = MASK && m == -__builtin_inff() ? 0.0f : -m;
       float psum = 0.f;
       f16x8 pf[2];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float e = __builtin_amdgcn_exp2f(fmaf(s4[kb][r], p.scale_log2, -m));
+          const float e = __builtin_amdgcn_exp2f(fmaf(s4[kb][r], p.scale_log2, mneg));
           psum += e;
           pf[kb >> 1][4 * (kb & 1) + r] = (f16)e;
         }
@@ -435,6 +482,7 @@ __global__ __launch_bounds__(256) void fa_fwd_f32_kernel(AttnParams p) {
   const int qrow = blockIdx.x * QPB + tid / TPQ;
   const bool qvalid = qrow < p.Sq;
   const float scale = p.scale_log2;
+  const uint8_t *mrow = p.mask ? mask_row(p, b, h, qvalid ? qrow : 0) : nullptr;
 
   float q[32], acc[32];
 #pragma unroll
@@ -462,18 +510,22 @@ __global__ __launch_bounds__(256) void fa_fwd_f32_kernel(AttnParams p) {
       for (int i = 0; i < 32; ++i) d = fmaf(q[i], Ks[j][part * 32 + i], d);
 #pragma unroll
       for (int o = 1; o < TPQ; o <<= 1) d += __shfl_xor(d, o, 64);
-      s[j] = (t * KT + j < L) ? d * scale : -__builtin_inff();
+      const int key = t * KT + j;
+      s[j] = key < L && (!mrow || mrow[key]) ? d * scale : -__builtin_inff();
       tmax = fmaxf(tmax, s[j]);
     }
+    // a query whose keys so far are all masked keeps m = -inf: no rescale,
+    // and exp2(-inf - 0) = 0 for its scores
     const float m_new = fmaxf(m, tmax);
-    const float alpha = exp2f(m - m_new);
+    const float alpha = m_new == -__builtin_inff() ? 1.0f : exp2f(m - m_new);
     m = m_new;
     l *= alpha;
 #pragma unroll
     for (int i = 0; i < 32; ++i) acc[i] *= alpha;
+    const float mref = m == -__builtin_inff() ? 0.0f : m;
 #pragma unroll
     for (int j = 0; j < KT; ++j) {
-      const float e = exp2f(s[j] - m);
+      const float e = exp2f(s[j] - mref);
       l += e;
 #pragma unroll
       for (int i = 0; i < 32; ++i) acc[i] = fmaf(e, Vs[j][part * 32 + i], acc[i]);
@@ -487,8 +539,8 @@ __global__ __launch_bounds__(256) void fa_fwd_f32_kernel(AttnParams p) {
   }
 }
 
-template <int D, bool PAD = false>
-static void launch_f16(const AttnParams &p, hipStream_t s) {
+template <int D, bool PAD = false, bool MASK = false>
+static void launch_f16_m(const AttnParams &p, hipStream_t s) {
   // 4 wavefronts x 32 queries per workgroup: at seq 128 one workgroup holds a
   // whole (batch, head), so K and V are read from HBM once.
   // Up to 128 queries (BERT s128), D = 64: 16-query wavefronts, 4 per
@@ -502,17 +554,23 @@ static void launch_f16(const AttnParams &p, hipStream_t s) {
       // (TPS = 2) was 0.7% slower per encoder step, fp16 and INT8-FFN, in
       // both-order A/Bs on two boxes.
       dim3 grid((unsigned)((p.Sq + 63) / 64), (unsigned)p.H, (unsigned)p.B);
-      fa_fwd_f16_q16_kernel<4, 1><<<grid, 256, 0, s>>>(p);
+      fa_fwd_f16_q16_kernel<4, 1, MASK><<<grid, 256, 0, s>>>(p);
       return;
     }
   }
   if (p.Sq >= 128) {
     dim3 grid((unsigned)((p.Sq + 127) / 128), (unsigned)p.H, (unsigned)p.B);
-    fa_fwd_f16_kernel<D, 4, PAD><<<grid, 256, 0, s>>>(p);
+    fa_fwd_f16_kernel<D, 4, PAD, MASK><<<grid, 256, 0, s>>>(p);
   } else {
     dim3 grid((unsigned)((p.Sq + 63) / 64), (unsigned)p.H, (unsigned)p.B);
-    fa_fwd_f16_kernel<D, 2, PAD><<<grid, 128, 0, s>>>(p);
+    fa_fwd_f16_kernel<D, 2, PAD, MASK><<<grid, 128, 0, s>>>(p);
   }
+}
+
+template <int D, bool PAD = false>
+static void launch_f16(const AttnParams &p, hipStream_t s) {
+  if (p.mask) launch_f16_m<D, PAD, true>(p, s);
+  else launch_f16_m<D, PAD, false>(p, s);
 }
 
 template <int D>
@@ -526,27 +584,24 @@ static void launch_f32(const AttnParams &p, hipStream_t s) {
 
 using namespace zk;
 
-extern "C" int zk_flash_attn_fwd(const void *Q, const void *K, const void *V,
-                                 void *O, int64_t batch, int64_t heads,
-                                 int64_t seq_q, int64_t seq_k,
-                                 int64_t head_dim, const int64_t *strides,
-                                 const int32_t *valid_lens, float scale,
-                                 int dtype, void *stream) {
+static int attn_impl(const char *who, const void *Q, const void *K, const void *V, void *O,
+                     int64_t batch, int64_t heads, int64_t seq_q, int64_t seq_k,
+                     int64_t head_dim, const int64_t *strides, const int32_t *valid_lens,
+                     const uint8_t *mask, const int64_t *mask_strides, float scale, int dtype,
+                     void *stream) {
   if (batch < 0 || heads < 0 || seq_q < 0 || seq_k < 0 || head_dim <= 0)
-    return fail(ZK_ERR_INVALID, "zk_flash_attn_fwd: bad size");
+    return fail(ZK_ERR_INVALID, "%s: bad size", who);
   if (batch == 0 || heads == 0 || seq_q == 0) return ZK_OK;
-  if (!Q || !K || !V || !O || !strides)
-    return fail(ZK_ERR_INVALID, "zk_flash_attn_fwd: null pointer");
+  if (!Q || !K || !V || !O || !strides) return fail(ZK_ERR_INVALID, "%s: null pointer", who);
   if (batch > 65535 || heads > 65535 || seq_q > 0x7fffffff || seq_k > 0x7fffffff)
-    return fail(ZK_ERR_UNSUPPORTED, "zk_flash_attn_fwd: size exceeds launch limits");
+    return fail(ZK_ERR_UNSUPPORTED, "%s: size exceeds launch limits", who);
   // any head_dim up to 128, the reference's HEAD_DIM_MAX (flash_attention.cu:26)
   if (head_dim > 128)
-    return fail(ZK_ERR_UNSUPPORTED, "zk_flash_attn_fwd: head_dim %lld > 128",
-                (long long)head_dim);
+    return fail(ZK_ERR_UNSUPPORTED, "%s: head_dim %lld > 128", who, (long long)head_dim);
   if (!(scale > 0.0f) || scale == __builtin_inff())
-    return fail(ZK_ERR_INVALID, "zk_flash_attn_fwd: scale must be finite and > 0");
+    return fail(ZK_ERR_INVALID, "%s: scale must be finite and > 0", who);
   for (int i = 0; i < 12; ++i)
-    if (strides[i] < 0) return fail(ZK_ERR_INVALID, "zk_flash_attn_fwd: negative stride");
+    if (strides[i] < 0) return fail(ZK_ERR_INVALID, "%s: negative stride", who);
   AttnParams p;
   p.Q = Q; p.K = K; p.V = V; p.O = O;
   p.B = (int)batch; p.H = (int)heads; p.Sq = (int)seq_q; p.Sk = (int)seq_k;
@@ -556,18 +611,30 @@ extern "C" int zk_flash_attn_fwd(const void *Q, const void *K, const void *V,
     p.sv[i] = strides[6 + i]; p.so[i] = strides[9 + i];
   }
   p.valid_lens = valid_lens;
+  p.mask = mask;
+  p.sm[0] = p.sm[1] = p.sm[2] = 0;
+  if (mask) {
+    if (!mask_strides) return fail(ZK_ERR_INVALID, "%s: mask without strides", who);
+    for (int i = 0; i < 3; ++i) {
+      if (mask_strides[i] < 0) return fail(ZK_ERR_INVALID, "%s: negative mask stride", who);
+      if (mask_strides[i] % 4)
+        return fail(ZK_ERR_UNSUPPORTED, "%s: mask strides must be multiples of 4", who);
+      p.sm[i] = mask_strides[i];
+    }
+    if (reinterpret_cast<uintptr_t>(mask) & 3u)
+      return fail(ZK_ERR_UNSUPPORTED, "%s: mask must be 4-byte aligned", who);
+  }
   p.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t s = as_stream(stream);
   if (dtype == ZK_F16) {
     for (int i = 0; i < 12; ++i)
       if (strides[i] % 8)
-        return fail(ZK_ERR_UNSUPPORTED, "zk_flash_attn_fwd: fp16 strides must be multiples of 8");
+        return fail(ZK_ERR_UNSUPPORTED, "%s: fp16 strides must be multiples of 8", who);
     if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O))
-      return fail(ZK_ERR_UNSUPPORTED, "zk_flash_attn_fwd: fp16 tensors must be 16-byte aligned");
+      return fail(ZK_ERR_UNSUPPORTED, "%s: fp16 tensors must be 16-byte aligned", who);
     if (head_dim % 8)
-      return fail(ZK_ERR_UNSUPPORTED,
-                  "zk_flash_attn_fwd: fp16 head_dim must be a multiple of 8 (got %lld)",
-                  (long long)head_dim);
+      return fail(ZK_ERR_UNSUPPORTED, "%s: fp16 head_dim must be a multiple of 8 (got %lld)",
+                  who, (long long)head_dim);
     // compiled widths 32 / 64 / 128; narrower head_dims are zero-padded
     if (head_dim == 32) launch_f16<32>(p, s);
     else if (head_dim == 64) launch_f16<64>(p, s);
@@ -580,7 +647,27 @@ extern "C" int zk_flash_attn_fwd(const void *Q, const void *K, const void *V,
     else if (head_dim <= 64) launch_f32<64>(p, s);
     else launch_f32<128>(p, s);
   } else {
-    return fail(ZK_ERR_UNSUPPORTED, "zk_flash_attn_fwd: dtype %d not supported", dtype);
+    return fail(ZK_ERR_UNSUPPORTED, "%s: dtype %d not supported", who, dtype);
   }
-  return check_launch("zk_flash_attn_fwd");
+  return check_launch(who);
+}
+
+extern "C" int zk_flash_attn_fwd(const void *Q, const void *K, const void *V, void *O,
+                                 int64_t batch, int64_t heads, int64_t seq_q, int64_t seq_k,
+                                 int64_t head_dim, const int64_t *strides,
+                                 const int32_t *valid_lens, float scale, int dtype,
+                                 void *stream) {
+  return attn_impl("zk_flash_attn_fwd", Q, K, V, O, batch, heads, seq_q, seq_k, head_dim,
+                   strides, valid_lens, nullptr, nullptr, scale, dtype, stream);
+}
+
+extern "C" int zk_flash_attn_fwd_masked(const void *Q, const void *K, const void *V, void *O,
+                                        int64_t batch, int64_t heads, int64_t seq_q,
+                                        int64_t seq_k, int64_t head_dim, const int64_t *strides,
+                                        const int32_t *valid_lens, const uint8_t *mask,
+                                        const int64_t *mask_strides, float scale, int dtype,
+                                        void *stream) {
+  if (!mask) return fail(ZK_ERR_INVALID, "zk_flash_attn_fwd_masked: null mask");
+  return attn_impl("zk_flash_attn_fwd_masked", Q, K, V, O, batch, heads, seq_q, seq_k,
+                   head_dim, strides, valid_lens, mask, mask_strides, scale, dtype, stream);
 }

@@ -277,20 +277,36 @@ def _meta_last_dim(node):
     return None
 
 
+def _meta_dtype(node):
+    for key in ("val", "example_value", "tensor_meta"):
+        v = node.meta.get(key) if isinstance(node, torch.fx.Node) else None
+        dt = getattr(v, "dtype", None)
+        if dt is not None:
+            return dt
+    return None
+
+
 def _as_sdpa(node):
-    """(q, k, v, scale) of an unmasked, non-causal, dropout-free
-    scaled_dot_product_attention, else None."""
+    """(q, k, v, scale, attn_mask) of a non-causal, dropout-free
+    scaled_dot_product_attention whose mask is absent or boolean (True =
+    attend; known from the graph's shape metadata, as torch.compile graphs
+    carry it: HF BERT's SDPA path passes a boolean [B, 1, Sq, Sk] padding
+    mask), else None. Additive float masks, and masks of unknown dtype, stay
+    with torch."""
     if node.op != "call_function" or node.target is not F.scaled_dot_product_attention:
         return None
     q, k, v = node.args[:3]
-    if _arg(node, 3, "attn_mask") is not None or _arg(node, 5, "is_causal", False):
+    mask = _arg(node, 3, "attn_mask")
+    if _arg(node, 5, "is_causal", False):
         return None
-    if float(_arg(node, 4, "dropout_p", 0.0) or 0.0) != 0.0 or node.kwargs.get("enable_gqa"):
+    if mask is not None and (not isinstance(mask, torch.fx.Node) or _meta_dtype(mask) != torch.bool):
+        return None
+    if float(_arg(node, 4, "dropout_p", 0.0) or 0.0) != 0.0 or _arg(node, 7, "enable_gqa", False):
         return None
     d = _meta_last_dim(q)
     if d is not None and d > _MAX_HEAD_DIM:
         return None
-    return [q, k, v, node.kwargs.get("scale")]
+    return [q, k, v, _arg(node, 6, "scale"), mask]
 
 
 def _feeds_gelu(node, mods) -> bool:

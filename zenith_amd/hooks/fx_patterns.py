@@ -192,8 +192,8 @@ def hip_linear(x, w, b):
 
 
 @torch.fx.wrap
-def hip_attention(q, k, v, scale):
-    return zenith_cuda.flash_attention(q, k, v, scale=scale)
+def hip_attention(q, k, v, scale, attn_mask=None):
+    return zenith_cuda.flash_attention(q, k, v, scale=scale, attn_mask=attn_mask)
 
 
 # ------------------------------------------------------------- registry ---

@@ -31,14 +31,29 @@ class TorchBertLayer(nn.Module):
                 mod.weight.copy_(torch.as_tensor(w[wk]))
                 mod.bias.copy_(torch.as_tensor(w[bk]))
 
-    def forward(self, x):
+    def _split(self, t, B, S):
+        return t.view(B, S, self.heads, -1).transpose(1, 2)
+
+    def _rest(self, a, x):
         B, S, H = x.shape
-        D = H // self.heads
-
-        def split(t):
-            return t.view(B, S, self.heads, D).transpose(1, 2)
-
-        a = F.scaled_dot_product_attention(split(self.q(x)), split(self.k(x)), split(self.v(x)))
         a = a.transpose(1, 2).reshape(B, S, H)
         h = self.ln1(self.o(a) + x)
         return self.ln2(self.o2(self.act(self.i(h))) + h)
+
+    def forward(self, x):
+        B, S, _ = x.shape
+        sp = lambda t: self._split(t, B, S)  # noqa: E731
+        return self._rest(F.scaled_dot_product_attention(sp(self.q(x)), sp(self.k(x)),
+                                                         sp(self.v(x))), x)
+
+
+class MaskedTorchBertLayer(TorchBertLayer):
+    """TorchBertLayer over a padded batch: forward(x, attn_mask) with the
+    boolean [B, 1, S, S] mask (True = attend) that HF BERT's SDPA attention
+    passes."""
+
+    def forward(self, x, attn_mask):
+        B, S, _ = x.shape
+        sp = lambda t: self._split(t, B, S)  # noqa: E731
+        return self._rest(F.scaled_dot_product_attention(sp(self.q(x)), sp(self.k(x)),
+                                                         sp(self.v(x)), attn_mask=attn_mask), x)

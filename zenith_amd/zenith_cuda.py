@@ -402,18 +402,51 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
 
 
 # --------------------------------------------------------------- attention --
+def _mask_arg(attn_mask: torch.Tensor, B: int, H: int, Sq: int, Sk: int):
+    """(uint8 tensor, (batch, head, query) byte strides) for a boolean mask
+    broadcastable to [B, H, Sq, Sk]: keys contiguous, rows 4-byte aligned and
+    padded to a multiple of 4 keys (copied only when the given layout is not
+    already so); broadcast dimensions get stride 0."""
+    if attn_mask.dtype != torch.bool:
+        raise RuntimeError("flash_attention: attn_mask must be boolean (True = attend); "
+                           "additive float masks are not supported")
+    if attn_mask.dim() > 4:
+        raise RuntimeError("flash_attention: attn_mask has more than 4 dimensions")
+    m = attn_mask.reshape((1,) * (4 - attn_mask.dim()) + tuple(attn_mask.shape))
+    for have, want in zip(m.shape, (B, H, Sq, Sk)):
+        if have not in (1, want):
+            raise RuntimeError(f"flash_attention: attn_mask {tuple(attn_mask.shape)} does not "
+                               f"broadcast to {(B, H, Sq, Sk)}")
+    if m.shape[3] != Sk:
+        m = m.expand(*m.shape[:3], Sk)
+    m = m.view(torch.uint8)
+    ok = (m.stride(3) == 1 and Sk % 4 == 0 and m.data_ptr() % 4 == 0 and
+          all(m.stride(i) % 4 == 0 or m.shape[i] == 1 for i in range(3)))
+    if not ok:
+        skp = (Sk + 3) // 4 * 4
+        dense = torch.zeros((*m.shape[:3], skp), dtype=torch.uint8, device=m.device)
+        dense[..., :Sk] = m
+        m = dense
+    strides = [0 if m.shape[i] == 1 else m.stride(i) for i in range(3)]
+    return m, strides
+
+
 def flash_attention(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor,
                     key_padding_lengths: torch.Tensor | None = None,
-                    scale: float | None = None) -> torch.Tensor:
+                    scale: float | None = None,
+                    attn_mask: torch.Tensor | None = None) -> torch.Tensor:
     """softmax(scale . Q K^T) V over [batch, heads, seq, head_dim] tensors,
     non-causal (reference flash_attention_forward, flash_attention.cu:327-340,
     scale 1/sqrt(head_dim)). `key_padding_lengths` (int, [batch]) masks keys
-    j >= length; a query with no valid key returns 0. fp32 and fp16; any
+    j >= length; `attn_mask` (bool, broadcastable to [batch, heads, seq_q,
+    seq_k], True = attend: scaled_dot_product_attention's boolean mask) masks
+    any (query, key) pair; both may be given. Masked keys get probability
+    exactly 0 and a query with no key left returns 0. fp32 and fp16; any
     head_dim up to 128 (HEAD_DIM_MAX, flash_attention.cu:26); fp16 head_dims
     that are not a multiple of 8 are zero-padded to one."""
     if not Q.is_cuda:
         raise RuntimeError("Q must be CUDA tensor")
-    _need_cuda(Q, K, V, key_padding_lengths)
+    _need_cuda(Q, K, V, key_padding_lengths, attn_mask)
     if Q.dim() != 4:
         raise RuntimeError("Q must be 4D [batch, heads, seq, dim]")
     if K.dim() != 4 or V.dim() != 4:
@@ -438,6 +471,7 @@ def flash_attention(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor,
         lens = key_padding_lengths.to(device=Q.device, dtype=torch.int32).contiguous()
         if lens.numel() != B:
             raise RuntimeError("key_padding_lengths must have one entry per batch")
+    mask = None if attn_mask is None else _mask_arg(attn_mask, B, H, Sq, Sk)
     if dt == L.ZK_F16 and D % 8:
         # zero columns add nothing to Q.K^T; V's give output columns dropped below
         Dp = (D + 7) // 8 * 8
@@ -446,22 +480,28 @@ def flash_attention(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor,
         Qp, Kp, Vp = pad(Q), pad(K), pad(V)
         _attn_call(Qp, Kp, Vp, O, B, H, Sq, Sk, Dp,
                    [*Qp.stride()[:3], *Kp.stride()[:3], *Vp.stride()[:3], *O.stride()[:3]],
-                   lens, scale, dt)
+                   lens, scale, dt, mask)
         return O[..., :D].contiguous()
     Q, K, V = lastdim(Q), lastdim(K), lastdim(V)
     O = torch.empty((B, H, Sq, D), dtype=Q.dtype, device=Q.device)
     return _attn_call(Q, K, V, O, B, H, Sq, Sk, D,
                       [*Q.stride()[:3], *K.stride()[:3], *V.stride()[:3], *O.stride()[:3]],
-                      lens, scale, dt)
+                      lens, scale, dt, mask)
 
 
-def _attn_call(Q, K, V, O, B, H, Sq, Sk, D, strides, lens, scale, dt):
+def _attn_call(Q, K, V, O, B, H, Sq, Sk, D, strides, lens, scale, dt, mask=None):
     if dt == L.ZK_F16 and (any(s % 8 for s in strides) or
                            any(t.data_ptr() % 16 for t in (Q, K, V, O))):
         Q, K, V = Q.contiguous(), K.contiguous(), V.contiguous()
         strides = [*Q.stride()[:3], *K.stride()[:3], *V.stride()[:3], *O.stride()[:3]]
-    L.call("zk_flash_attn_fwd", _p(Q), _p(K), _p(V), _p(O), B, H, Sq, Sk, D,
-           L.strides_arg(strides), _p(lens), float(scale), dt, _stream(Q))
+    if mask is None:
+        L.call("zk_flash_attn_fwd", _p(Q), _p(K), _p(V), _p(O), B, H, Sq, Sk, D,
+               L.strides_arg(strides), _p(lens), float(scale), dt, _stream(Q))
+    else:
+        m, ms = mask
+        L.call("zk_flash_attn_fwd_masked", _p(Q), _p(K), _p(V), _p(O), B, H, Sq, Sk, D,
+               L.strides_arg(strides), _p(lens), _p(m), L.strides_arg(ms), float(scale), dt,
+               _stream(Q))
     return O
 
 
