@@ -36,7 +36,8 @@ def _run(dev, q, k, v, lens, dtype):
 
 @pytest.mark.parametrize("B,H,S,D", [(2, 12, 128, 64), (2, 3, 512, 64), (3, 2, 77, 64),
                                      (2, 2, 130, 128), (2, 2, 64, 32), (1, 1, 1, 64),
-                                     (2, 4, 300, 64), (4, 2, 100, 64)])
+                                     (2, 4, 300, 64), (4, 2, 100, 64), (3, 2, 400, 64),
+                                     (2, 4, 777, 64), (2, 2, 600, 48)])
 @pytest.mark.parametrize("masked", [False, True])
 def test_flash_attention_f16(dev, B, H, S, D, masked):
     """B*H a multiple of 8 with 2 and 3 query blocks per head exercises the
@@ -129,7 +130,7 @@ def _mask_case(kind, B, H, S, rng):
 
 
 @pytest.mark.parametrize("B,H,S,D", [(2, 3, 128, 64), (2, 2, 300, 64), (2, 2, 77, 48),
-                                     (1, 2, 130, 128), (2, 2, 64, 32)])
+                                     (1, 2, 130, 128), (2, 2, 64, 32), (1, 2, 520, 64)])
 @pytest.mark.parametrize("kind", ["hf_padding", "keys_only", "per_query", "shared_2d"])
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
 def test_flash_attention_bool_mask(dev, B, H, S, D, kind, dtype):

@@ -558,6 +558,21 @@ static void launch_f16_m(const AttnParams &p, hipStream_t s) {
       return;
     }
   }
+  // From 384 queries on (s512), 8 wavefronts (256 queries) per workgroup:
+  // each staged K/V tile then serves twice the queries. The kernel is bound
+  // by per-wave latency and occupancy (VALU 46% and matrix cores 19% busy at
+  // 1.8 resident waves per SIMD), not by LDS bandwidth: at b32 s512 this
+  // takes 42.2-42.9 us against 45.5-47.6 us with 4 wavefronts, while two
+  // 32-query blocks per wavefront (half the LDS traffic per query, but 1-2
+  // waves per SIMD) took 53-61 us. At 256 queries it would leave one
+  // workgroup per (batch, head) and is slower (19.5 against 17.4 us).
+  if constexpr (D == 64) {
+    if (p.Sq >= 384) {
+      dim3 grid((unsigned)((p.Sq + 255) / 256), (unsigned)p.H, (unsigned)p.B);
+      fa_fwd_f16_kernel<D, 8, PAD, MASK><<<grid, 512, 0, s>>>(p);
+      return;
+    }
+  }
   if (p.Sq >= 128) {
     dim3 grid((unsigned)((p.Sq + 127) / 128), (unsigned)p.H, (unsigned)p.B);
     fa_fwd_f16_kernel<D, 4, PAD, MASK><<<grid, 256, 0, s>>>(p);
