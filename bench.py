@@ -14,7 +14,7 @@ replayed from a HIP graph, inputs resident in HBM. Prints ONE JSON line with:
                        out-projection, Add+LN, FFN-up, FFN-down), as measured
                        in the `kernels` table (HIP events on the launch
                        stream); `traffic` from its rocprofv3 FETCH_SIZE /
-                       WRITE_SIZE summary profiles/<name>_pmc.md when present
+                       WRITE_SIZE summary profiles/hbm_traffic_pmc.md
   kernels              per-kernel times and roofline fractions for the
                        workload configs: FP16 GEMM sweep (config 2), flash
                        attention s128 / s512 (config 3), INT8 FFN GEMMs
@@ -325,16 +325,19 @@ def measure_kernels(torch, dev, names=None):
     return out
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.md")
+
+
 def pmc_traffic(name: str):
-    """HBM bytes per launch of kernel case `name` from its committed
-    rocprofv3 counter summary profiles/<name>_pmc.md (FETCH_SIZE + WRITE_SIZE,
-    each scaled by the copy-kernel calibration); None when it is absent."""
-    path = os.path.join(ROOT, "profiles", f"{name}_pmc.md")
+    """HBM bytes per launch of kernel case `name` from the committed
+    rocprofv3 counter summary (EA read requests + WRITE_SIZE, each scaled by
+    the copy-kernel calibration), read from its `hbm_bytes_per_launch[name]:`
+    line; None when the file or the line is absent."""
     try:
-        txt = open(path).read()
+        txt = open(TRAFFIC_PROFILE).read()
     except OSError:
         return None
-    m = re.search(r"hbm_bytes_per_launch:\s*([0-9.eE+]+)", txt)
+    m = re.search(r"hbm_bytes_per_launch\[" + re.escape(name) + r"\]:\s*([0-9.eE+]+)", txt)
     return float(m.group(1)) if m else None
 
 
