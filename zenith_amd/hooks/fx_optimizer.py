@@ -19,8 +19,9 @@ Differences:
     models and torch.compile graphs contain, which the literal patterns
     cannot match: nn.Linear / nn.LayerNorm / nn.GELU modules, F.layer_norm
     with a constant normalized shape, F.scaled_dot_product_attention
-    without mask or dropout. Where the graph carries shape metadata, an
-    attention whose head_dim the kernel does not support is left alone.
+    without dropout or causal flag, unmasked or with a boolean mask. Where
+    the graph carries shape metadata, an attention whose head_dim exceeds
+    the kernel's 128 is left alone.
 """
 
 from __future__ import annotations
