@@ -72,6 +72,14 @@ __device__ __forceinline__ AttnTile attn_tile() {
   return {(int)(rem / 8), (int)(bh % nh), (int)(bh / nh)};
 }
 
+// max(a, b) of scores that are never NaN, as v_med3(a, b, +inf). Chains of
+// these compile to v_max3_f32 alone; fmaxf on MFMA results also makes a
+// NaN-quieting copy of every operand (32 extra VALU instructions per
+// 32 x 64 score tile of a wavefront).
+__device__ __forceinline__ float smax(float a, float b) {
+  return __builtin_amdgcn_fmed3f(a, b, __builtin_inff());
+}
+
 // ds_read_b64_tr_b16: 8 bytes per lane, transposed across each group of 16
 // lanes (see its use below for the lane mapping).
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -218,9 +226,9 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) tmax = fmaxf(tmax, fmaxf(s[kb][r], s[kb][r + 1]));
+      for (int r = 0; r < 16; ++r) tmax = smax(tmax, s[kb][r]);
     // finite unless MASK (without a mask, key t*KT < L is valid)
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * p.scale_log2;
+    tmax = smax(tmax, __shfl_xor(tmax, 32, 64)) * p.scale_log2;
     // Lazy rescaling: the reference point m (log2 units) only moves when the
     // tile max exceeds it by more than 8, so exp2(s - m) <= 256 always fits
     // fp16 and the accumulator is rescaled on a few tiles only. O / l is
@@ -408,10 +416,10 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_q16_kernel(AttnParams p) {
       float tmax = -__builtin_inff();
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
-        tmax = fmaxf(tmax, fmaxf(fmaxf(s4[kb][0], s4[kb][1]), fmaxf(s4[kb][2], s4[kb][3])));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = smax(smax(tmax, s4[kb][0]), smax(s4[kb][1], smax(s4[kb][2], s4[kb][3])));
+      tmax = smax(tmax, __shfl_xor(tmax, 16, 64));
       // finite unless MASK (without a mask, key t*KT < L is valid)
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * p.scale_log2;
+      tmax = smax(tmax, __shfl_xor(tmax, 32, 64)) * p.scale_log2;
       if (__builtin_amdgcn_ballot_w64(tmax > m + 8.0f) != 0) {
         const float m_new = fmaxf(m, tmax);
         const float alpha = MASK && m_new == -__builtin_inff() ? 1.0f
