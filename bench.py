@@ -10,8 +10,9 @@ replayed from a HIP graph, inputs resident in HBM. Prints ONE JSON line with:
                        same fp16 encoder at seq 512, config 5's other
                        length, in `encoder_s512`)
   roofline             the dominant kernel of the timed step: the longest of
-                       the kernels one encoder layer launches (QKV, attention,
-                       out-projection, Add+LN, FFN-up, FFN-down), as measured
+                       the kernels one encoder layer launches (fused QKV
+                       projection + attention, out-projection, Add+LN,
+                       FFN-up, FFN-down), as measured
                        in the `kernels` table (HIP events on the launch
                        stream); `traffic` from its rocprofv3 FETCH_SIZE /
                        WRITE_SIZE summary profiles/hbm_traffic_pmc.md
@@ -193,6 +194,24 @@ def kernel_cases(torch, dev):
                 f"B={B} H={H} S={S} D={D} lens~U{{S/2..S}} (dense FLOPs)"
         return setup
 
+    def qkv_attn(B=32, S=128, heads=12):
+        """The encoder's fused QKV projection + attention (one launch per
+        layer at s128): the QKV GEMM FLOPs plus the dense attention FLOPs."""
+        def setup():
+            H = heads * 64
+            x = torch.from_numpy(synthetic.normal((B * S, H), tag=70)).to(dev, f16)
+            w = torch.from_numpy(synthetic.normal((3 * H, H), tag=71, std=0.05)).to(dev, f16)
+            b = torch.from_numpy(synthetic.normal((3 * H,), tag=72, std=0.1)).to(dev, f16)
+            ctx = torch.empty((B * S, H), dtype=f16, device=dev)
+            lens = torch.from_numpy(synthetic.padding_lengths(B, S)).to(dev)
+            keep = (x, w, b, ctx, lens)
+            args = (x.data_ptr(), w.data_ptr(), b.data_ptr(), ctx.data_ptr(), B, S, H, heads,
+                    lens.data_ptr(), 1.0 / math.sqrt(64))
+            return (lambda i: _rc(L, lib.zk_qkv_attn_f16(*args, s())) and keep), \
+                2.0 * B * S * 3 * H * H + 4.0 * B * heads * S * S * 64, "TFLOP/s", "fp16", "mfma", \
+                f"B={B} S={S} heads={heads} M={B * S} K={H} N={3 * H} + attention (dense FLOPs)"
+        return setup
+
     def add_ln(M=4096):
         def setup():
             H = 768
@@ -276,6 +295,7 @@ def kernel_cases(torch, dev):
         "gemm_sq4096": gemm(4096, 4096, 4096, L.ZK_EPI_NONE),
         "gemm_sq8192": gemm(8192, 8192, 8192, L.ZK_EPI_NONE),
         "attn_s128": attn(128),
+        "qkv_attn_s128": qkv_attn(),
         "attn_s512": attn(512),
         "int8_ffn_up": gemm_i8(4096, 768, 3072, L.ZK_EPI_BIAS_GELU_ERF, requant=True),
         "int8_ffn_down": gemm_i8(4096, 3072, 768, E),
@@ -294,7 +314,7 @@ def kernel_cases(torch, dev):
 
 # kernels one step of the timed encoder (b32 s128) launches, per layer: the
 # roofline line names the longest of them
-STEP_KERNELS = ("gemm_qkv", "attn_s128", "gemm_out_proj", "add_layernorm", "gemm_ffn_up",
+STEP_KERNELS = ("qkv_attn_s128", "gemm_out_proj", "add_layernorm", "gemm_ffn_up",
                 "gemm_ffn_down")
 KERNEL_DESC = {
     "gemm_qkv": "gemm_mfma_kernel<F16Op, bias> M=4096 K=768 N=2304 (QKV)",
@@ -302,6 +322,8 @@ KERNEL_DESC = {
     "gemm_ffn_up": "gemm_mfma_kernel<F16Op, bias+gelu_erf> M=4096 K=768 N=3072 (FFN-up)",
     "gemm_ffn_down": "gemm_mfma_kernel<F16Op, bias> M=4096 K=3072 N=768 (FFN-down)",
     "attn_s128": "fa_fwd_f16_q16_kernel B=32 H=12 S=128 D=64, key padding",
+    "qkv_attn_s128": "gemm_mfma_kernel<F16Op, QKV + attention epilogue> M=4096 K=768 N=2304 "
+                     "+ attention B=32 H=12 S=128 D=64 (fused QKV projection and attention)",
     "add_layernorm": "ln_wave_kernel fp16 [4096,768] with residual",
 }
 

@@ -142,6 +142,27 @@ int zk_gemm_f32(const float *A, const float *B, float *C, int64_t M,
                 int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
                 int trans_b, void *stream);
 
+/* Fused QKV projection + attention for sequences of 64 or 128 tokens and
+ * head_dim 64, fp16:
+ *   qkv = X[B*S, H] . Wqkv^T + bqkv   (Wqkv [3H, H] with the rows of each
+ *                                      head interleaved: q_h, k_h, v_h,
+ *                                      64 rows each, h = 0 .. heads-1)
+ *   ctx[b*S + s, 64h .. 64h+63] = softmax(scale * q . k^T) . v per (b, h),
+ *                                 keys j >= valid_lens[b] masked as in
+ *                                 zk_flash_attn_fwd (valid_lens may be NULL)
+ * Q, K and V stay on chip: each 256-row x 192-column GEMM tile holds one
+ * head of 256 / S whole sequences and runs their attention in its epilogue.
+ * The values equal the unfused pair zk_gemm_f16 (bias epilogue, fp16 out)
+ * + zk_flash_attn_fwd to fp16 rounding of the attention output. H must be
+ * heads * 64; X and Wqkv 16-byte aligned, ctx 8-byte aligned, rows dense.
+ * No single reference counterpart: replaces the QKV linear_fp16_gpu calls,
+ * the transposes and attention_full_fp16_gpu of the reference encoder layer
+ * (benchmarks/bert_fp16_full.py:98-121), i.e. zenith_cuda.wmma_matmul and
+ * zenith_cuda.flash_attention (cuda_bindings.cpp:90-132). */
+int zk_qkv_attn_f16(const void *X, const void *Wqkv, const void *bqkv, void *ctx,
+                    int64_t batch, int64_t seq, int64_t hidden, int64_t heads,
+                    const int32_t *valid_lens, float scale, void *stream);
+
 /* Flash-attention forward, non-causal, online softmax with fp32 statistics.
  *   O[b,h,s,:] = softmax(scale * Q[b,h,s,:] . K[b,h,:,:]^T) . V[b,h,:,:]
  * Tensors are addressed by strides (elements): strides[0..2] are the

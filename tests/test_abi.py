@@ -66,6 +66,18 @@ def test_library_exports_every_declared_symbol():
                                 L.ZK_I32, None), L.ZK_ERR_UNSUPPORTED),  # int8 span
     (lambda lib: lib.zk_gemm_i8_requant(16, 16, 16, 8, 8, 16, 16, 1 << 24, 8, 1.0, 16, None, 0,
                                         1.0, None), L.ZK_ERR_UNSUPPORTED),  # int8 span (W)
+    (lambda lib: lib.zk_qkv_attn_f16(16, 16, 16, 16, 2, 96, 768, 12, None, 0.125, None),
+     L.ZK_ERR_UNSUPPORTED),  # fused QKV + attention: seq 64 or 128 only
+    (lambda lib: lib.zk_qkv_attn_f16(16, 16, 16, 16, 2, 128, 768, 6, None, 0.125, None),
+     L.ZK_ERR_UNSUPPORTED),  # head dim 128
+    (lambda lib: lib.zk_qkv_attn_f16(16, None, 16, 16, 2, 128, 768, 12, None, 0.125, None),
+     L.ZK_ERR_INVALID),
+    (lambda lib: lib.zk_qkv_attn_f16(16, 16, 16, 16, 2, 128, 768, 12, None, 0.0, None),
+     L.ZK_ERR_INVALID),
+    (lambda lib: lib.zk_qkv_attn_f16(16, 16, 16, 16, -1, 128, 768, 12, None, 0.125, None),
+     L.ZK_ERR_INVALID),
+    (lambda lib: lib.zk_qkv_attn_f16(16, 16, 16, 12, 2, 128, 768, 12, None, 0.125, None),
+     L.ZK_ERR_UNSUPPORTED),  # ctx not 8-byte aligned
     (lambda lib: lib.zk_layernorm_add(16, None, 16, 16, 16, 4, 8, 1e-5, L.ZK_F32, None),
      L.ZK_ERR_INVALID),  # LayerNormAdd needs its residual
     (lambda lib: lib.zk_layernorm_add(16, 16, 16, 16, 16, 4, 8, 1e-5, L.ZK_I8, None),

@@ -51,6 +51,7 @@ SIGNATURES: dict[str, list] = {
     "zk_gemm_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _vp],
     "zk_linear_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _i32,
                       _vp, _i64, _vp],
+    "zk_qkv_attn_f16": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _f32, _vp],
     "zk_flash_attn_fwd": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                           ctypes.POINTER(_i64), _vp, _f32, _i32, _vp],
     "zk_flash_attn_fwd_masked": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,

@@ -41,7 +41,7 @@
 
 #include <type_traits>
 
-#include "zk_common.hpp"
+#include "zk_attn_tile.hpp"
 
 namespace zk {
 
@@ -66,7 +66,17 @@ struct GemmParams {
   int splits;
   int nk_per;
   int64_t split_stride;
+  // fused QKV projection + attention (kEpiQkvAttn): sequences of `seq`
+  // rows, `batch` of them, key-padding lengths, softmax scale * log2(e)
+  int seq;
+  int batch;
+  const int32_t *valid_lens;
+  float scale_log2;
 };
+
+// Epilogue of the fused QKV projection + attention (internal; not one of the
+// public ZK_EPI_* values).
+constexpr int kEpiQkvAttn = 100;
 
 // MFMA step on 16 bytes per lane and operand. MS = 32: lane l supplies row
 // l % 32, bytes [16 * (l / 32), +16) of the 32-byte k-step; the result
@@ -386,99 +396,166 @@ void gemm_mfma_kernel(GemmParams p) {
   }
 #undef ZK_ISSUE
   __syncthreads();  // every wave is done reading the ring; it becomes epilogue space
-
-  // Epilogue: per wave, one MS-row stripe at a time.
-  float *ws = (float *)smem + wave * MS * G::EPITCH;
-  // int8 output (re-quantisation): bias and residual are fp16; the value is
-  // rounded to fp16 first, so the result equals quantising the fp16 output.
-  constexpr bool Q8 = std::is_same<OutT, int8_t>::value;
-  typedef typename std::conditional<Q8, f16, OutT>::type BiasT;
-  OutT *C = (OutT *)p.C + (p.splits > 1 ? split * p.split_stride : 0);
-  const BiasT *bias = (const BiasT *)p.bias;
-  const BiasT *res = (const BiasT *)p.res;
-  const float inv_q = Q8 ? 1.0f / p.s_q : 1.0f;
-  const bool vec_ok = (p.ldc % 8 == 0) && (Q8 ? aligned8(p.C) : aligned16(p.C)) &&
-                      (EPI != ZK_EPI_BIAS_RESIDUAL || ((p.ldr % 8 == 0) && aligned16(p.res)));
-  float bj[TN], sj[TN];
-#pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int col = n0 + wn * WTN + j * MS + frow;
-    bj[j] = 0.f;
-    sj[j] = 1.f;
-    if (col < p.N) {
-      if (EPI != ZK_EPI_NONE) bj[j] = to_f(bias[col]);
-      if (DEQ) sj[j] = p.s_x * p.s_w[col];
-    }
-  }
-  constexpr int VPR = WTN / 8;  // 8-column vectors per stripe row
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
+  if constexpr (EPI == kEpiQkvAttn) {
+    // The tile is the Q, K and V columns of head tn (weights interleaved
+    // per head: q, k, v, 64 rows each) for the 256 rows of the sequences
+    // the tile holds. They go into LDS as fp16 with their bias, [part][row]
+    // [64] with the K/V tile swizzle, and the tile's attention runs from
+    // there: Q, K and V never reach HBM.
+    static_assert(std::is_same<OP, F16Op>::value && BM == 256 && BN == 192 && MS == 32 &&
+                      WM == 4 && WN == 2, "fused QKV attention tile");
+    constexpr int HD = 64;
+    f16 *qkv = (f16 *)smem;  // 3 x 256 x 64 halves = 96 KB, inside the ring
+    const f16 *bias = (const f16 *)p.bias;
+    const int h32 = lane >> 5;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
+      const int cb = wn * WTN + j * 32;  // first tile column of the block
+      const int d = cb % HD + (lane & 31);
+      const float bv = to_f(bias[n0 + cb + (lane & 31)]);
+      f16 *dst = qkv + (cb / HD) * (BM * HD);
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int rl = MS == 32 ? 8 * (r >> 2) + 4 * fch + (r & 3) : 4 * fch + r;
-        float *dst = ws + rl * G::EPITCH + j * MS + frow;
-        if constexpr (std::is_same<OutT, int32_t>::value) {
-          *(int *)dst = acc[i][j][r];
-        } else {
-          const float v = DEQ ? (float)acc[i][j][r] * sj[j] : (float)acc[i][j][r];
-          *dst = epilogue<EPI>(v, bj[j]);
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = wm * WTM + i * 32 + 8 * (r >> 2) + 4 * h32 + (r & 3);
+          dst[row * HD + (((d >> 3) ^ kv_swz(row)) << 3) + (d & 7)] = (f16)(acc[i][j][r] + bv);
         }
+    }
+    __syncthreads();
+    // Wave w owns the 32 queries of tile rows [32 w, 32 w + 32); their
+    // sequence's keys are tile rows [sq * seq, +seq).
+    const int qr = wave * 32 + (lane & 31);
+    const int sq = wave * 32 / p.seq;
+    const int b = m0 / p.seq + sq;
+    if (b < p.batch) {
+      int L = p.valid_lens ? p.valid_lens[b] : p.seq;
+      L = L < 0 ? 0 : (L > p.seq ? p.seq : L);
+      f16x8 qf[HD / 16];
+#pragma unroll
+      for (int c = 0; c < HD / 16; ++c)
+        qf[c] = *(const f16x8 *)(qkv + qr * HD + (((2 * c + h32) ^ kv_swz(qr)) << 3));
+      const f16 *Kt = qkv + BM * HD + sq * p.seq * HD, *Vt = Kt + BM * HD;
+      f32x16 o[HD / 32];
+#pragma unroll
+      for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
+      float m = -__builtin_inff(), l = 0.f;
+      const int ntiles = (L + 63) / 64;
+      for (int t = 0; t < ntiles; ++t)
+        attn32_tile<HD, true, HD, false>(Kt + t * 64 * HD, Vt + t * 64 * HD, qf, t, L,
+                                         p.scale_log2, nullptr, nullptr, lane, o, m, l);
+      const int grow = m0 + qr;
+      if (grow < p.M) {
+        const float inv = l > 0.f ? 1.0f / l : 0.f;
+        f16 *O = (f16 *)p.C + (int64_t)grow * p.ldc + tn * HD;
+#pragma unroll
+        for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            f16x4 out;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) out[e] = (f16)(o[dt][4 * g + e] * inv);
+            *(f16x4 *)(O + dt * 32 + 8 * g + 4 * h32) = out;
+          }
       }
     }
-    const int row0 = m0 + wm * WTM + i * MS, col0 = n0 + wn * WTN;
-    for (int v = lane; v < MS * VPR; v += 64) {
-      const int rl = v / VPR, cl = (v % VPR) * 8;
-      const int row = row0 + rl, col = col0 + cl;
-      if (row >= p.M || col >= p.N) continue;
-      const float *src = ws + rl * G::EPITCH + cl;
-      OutT *dst = C + (int64_t)row * p.ldc + col;
-      if (vec_ok && col + 8 <= p.N) {
-        const f32x4 lo = *(const f32x4 *)src, hi = *(const f32x4 *)(src + 4);
-        if constexpr (std::is_same<OutT, int32_t>::value) {
-          *(f32x4 *)dst = lo;  // raw bits of the int32 accumulators
-          *(f32x4 *)(dst + 4) = hi;
-        } else {
-          float o[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          if constexpr (EPI == ZK_EPI_BIAS_RESIDUAL) {
-            const BiasT *rp = res + (int64_t)row * p.ldr + col;
-            if constexpr (std::is_same<BiasT, f16>::value) {
-              const f16x8 rv = *(const f16x8 *)rp;
-#pragma unroll
-              for (int e = 0; e < 8; ++e) o[e] += (float)rv[e];
-            } else {
-#pragma unroll
-              for (int e = 0; e < 8; ++e) o[e] += to_f(rp[e]);
-            }
-          }
-          if constexpr (std::is_same<OutT, f16>::value) {
-            f16x8 h;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) h[e] = (f16)o[e];
-            store_nt((f16x8 *)dst, h);
-          } else if constexpr (Q8) {
-            uint32_t qlo = 0, qhi = 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              qlo |= (uint32_t)(uint8_t)quant1((float)(f16)o[e], p.s_q, inv_q) << (8 * e);
-              qhi |= (uint32_t)(uint8_t)quant1((float)(f16)o[e + 4], p.s_q, inv_q) << (8 * e);
-            }
-            store_nt((u32x2 *)dst, u32x2{qlo, qhi});
+  } else {
+
+    // Epilogue: per wave, one MS-row stripe at a time.
+    float *ws = (float *)smem + wave * MS * G::EPITCH;
+    // int8 output (re-quantisation): bias and residual are fp16; the value is
+    // rounded to fp16 first, so the result equals quantising the fp16 output.
+    constexpr bool Q8 = std::is_same<OutT, int8_t>::value;
+    typedef typename std::conditional<Q8, f16, OutT>::type BiasT;
+    OutT *C = (OutT *)p.C + (p.splits > 1 ? split * p.split_stride : 0);
+    const BiasT *bias = (const BiasT *)p.bias;
+    const BiasT *res = (const BiasT *)p.res;
+    const float inv_q = Q8 ? 1.0f / p.s_q : 1.0f;
+    const bool vec_ok = (p.ldc % 8 == 0) && (Q8 ? aligned8(p.C) : aligned16(p.C)) &&
+                        (EPI != ZK_EPI_BIAS_RESIDUAL || ((p.ldr % 8 == 0) && aligned16(p.res)));
+    float bj[TN], sj[TN];
+  #pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = n0 + wn * WTN + j * MS + frow;
+      bj[j] = 0.f;
+      sj[j] = 1.f;
+      if (col < p.N) {
+        if (EPI != ZK_EPI_NONE) bj[j] = to_f(bias[col]);
+        if (DEQ) sj[j] = p.s_x * p.s_w[col];
+      }
+    }
+    constexpr int VPR = WTN / 8;  // 8-column vectors per stripe row
+  #pragma unroll
+    for (int i = 0; i < TM; ++i) {
+  #pragma unroll
+      for (int j = 0; j < TN; ++j) {
+  #pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int rl = MS == 32 ? 8 * (r >> 2) + 4 * fch + (r & 3) : 4 * fch + r;
+          float *dst = ws + rl * G::EPITCH + j * MS + frow;
+          if constexpr (std::is_same<OutT, int32_t>::value) {
+            *(int *)dst = acc[i][j][r];
           } else {
-            *(f32x4 *)dst = f32x4{o[0], o[1], o[2], o[3]};
-            *(f32x4 *)(dst + 4) = f32x4{o[4], o[5], o[6], o[7]};
+            const float v = DEQ ? (float)acc[i][j][r] * sj[j] : (float)acc[i][j][r];
+            *dst = epilogue<EPI>(v, bj[j]);
           }
         }
-      } else {
-        for (int e = 0; e < 8 && col + e < p.N; ++e) {
+      }
+      const int row0 = m0 + wm * WTM + i * MS, col0 = n0 + wn * WTN;
+      for (int v = lane; v < MS * VPR; v += 64) {
+        const int rl = v / VPR, cl = (v % VPR) * 8;
+        const int row = row0 + rl, col = col0 + cl;
+        if (row >= p.M || col >= p.N) continue;
+        const float *src = ws + rl * G::EPITCH + cl;
+        OutT *dst = C + (int64_t)row * p.ldc + col;
+        if (vec_ok && col + 8 <= p.N) {
+          const f32x4 lo = *(const f32x4 *)src, hi = *(const f32x4 *)(src + 4);
           if constexpr (std::is_same<OutT, int32_t>::value) {
-            dst[e] = ((const int *)src)[e];
+            *(f32x4 *)dst = lo;  // raw bits of the int32 accumulators
+            *(f32x4 *)(dst + 4) = hi;
           } else {
-            float o = src[e];
-            if (EPI == ZK_EPI_BIAS_RESIDUAL) o += to_f(res[(int64_t)row * p.ldr + col + e]);
-            if constexpr (Q8) dst[e] = quant1((float)(f16)o, p.s_q, inv_q);
-            else dst[e] = (OutT)o;
+            float o[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            if constexpr (EPI == ZK_EPI_BIAS_RESIDUAL) {
+              const BiasT *rp = res + (int64_t)row * p.ldr + col;
+              if constexpr (std::is_same<BiasT, f16>::value) {
+                const f16x8 rv = *(const f16x8 *)rp;
+  #pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] += (float)rv[e];
+              } else {
+  #pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] += to_f(rp[e]);
+              }
+            }
+            if constexpr (std::is_same<OutT, f16>::value) {
+              f16x8 h;
+  #pragma unroll
+              for (int e = 0; e < 8; ++e) h[e] = (f16)o[e];
+              store_nt((f16x8 *)dst, h);
+            } else if constexpr (Q8) {
+              uint32_t qlo = 0, qhi = 0;
+  #pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                qlo |= (uint32_t)(uint8_t)quant1((float)(f16)o[e], p.s_q, inv_q) << (8 * e);
+                qhi |= (uint32_t)(uint8_t)quant1((float)(f16)o[e + 4], p.s_q, inv_q) << (8 * e);
+              }
+              store_nt((u32x2 *)dst, u32x2{qlo, qhi});
+            } else {
+              *(f32x4 *)dst = f32x4{o[0], o[1], o[2], o[3]};
+              *(f32x4 *)(dst + 4) = f32x4{o[4], o[5], o[6], o[7]};
+            }
+          }
+        } else {
+          for (int e = 0; e < 8 && col + e < p.N; ++e) {
+            if constexpr (std::is_same<OutT, int32_t>::value) {
+              dst[e] = ((const int *)src)[e];
+            } else {
+              float o = src[e];
+              if (EPI == ZK_EPI_BIAS_RESIDUAL) o += to_f(res[(int64_t)row * p.ldr + col + e]);
+              if constexpr (Q8) dst[e] = quant1((float)(f16)o, p.s_q, inv_q);
+              else dst[e] = (OutT)o;
+            }
           }
         }
       }
@@ -800,6 +877,52 @@ extern "C" int zk_gemm_f16_ws(const void *A, const void *B, void *C, int64_t M, 
   if (ws_bytes < 0) return fail(ZK_ERR_INVALID, "zk_gemm_f16_ws: negative workspace size");
   return gemm_f16_impl(A, B, C, M, N, K, lda, ldb, ldc, trans_b, out_dtype, bias, residual, ldr,
                        epilogue, workspace, ws_bytes, stream);
+}
+
+// Fused QKV projection + attention (sequences of 64 or 128 tokens, head dim
+// 64): one 256 x 192 tile per workgroup, the q, k and v columns of one head
+// for 256 rows, with the attention of the tile's sequences in its epilogue.
+static void launch_qkv_attn(GemmParams p, hipStream_t s) {
+  p.tiles_n = p.N / 192;
+  p.tiles_m = (p.M + 255) / 256;
+  const int grid = p.tiles_m * p.tiles_n;
+  int gm = 1;
+  const int per_xcd = (grid + 7) / 8;
+  while (gm * 2 <= p.tiles_m && gm * gm * 4 <= per_xcd) gm *= 2;
+  p.group_m = gm;
+  gemm_mfma_kernel<F16Op, 256, 192, 32, 128, 2, 4, 2, kEpiQkvAttn, f16, false>
+      <<<grid, 512, 0, s>>>(p);
+}
+
+extern "C" int zk_qkv_attn_f16(const void *X, const void *Wqkv, const void *bqkv, void *ctx,
+                               int64_t batch, int64_t seq, int64_t hidden, int64_t heads,
+                               const int32_t *valid_lens, float scale, void *stream) {
+  const char *who = "zk_qkv_attn_f16";
+  if (batch < 0 || seq <= 0 || hidden <= 0 || heads <= 0)
+    return fail(ZK_ERR_INVALID, "%s: bad size", who);
+  if (batch == 0) return ZK_OK;
+  if (!X || !Wqkv || !bqkv || !ctx) return fail(ZK_ERR_INVALID, "%s: null pointer", who);
+  if (hidden != heads * 64)
+    return fail(ZK_ERR_UNSUPPORTED, "%s: head dim must be 64 (hidden %lld, heads %lld)", who,
+                (long long)hidden, (long long)heads);
+  if (seq != 64 && seq != 128)
+    return fail(ZK_ERR_UNSUPPORTED, "%s: seq must be 64 or 128 (got %lld)", who, (long long)seq);
+  if (!(scale > 0.0f) || scale == __builtin_inff())
+    return fail(ZK_ERR_INVALID, "%s: scale must be finite and > 0", who);
+  if (batch > 0x7fffffff / seq) return fail(ZK_ERR_UNSUPPORTED, "%s: batch * seq exceeds int32", who);
+  const int64_t M = batch * seq, N = 3 * hidden, K = hidden;
+  int st = check_dims(who, M, N, K);
+  if (st) return st;
+  if (!aligned16(X) || !aligned16(Wqkv) || !aligned8(ctx))
+    return fail(ZK_ERR_UNSUPPORTED, "%s: X and Wqkv must be 16-byte, ctx 8-byte aligned", who);
+  if ((st = check_span(who, K, K, K, 2))) return st;
+  GemmParams p{X, Wqkv, ctx, (int)M, (int)N, (int)K, K, K, hidden, bqkv, nullptr, 0, 1.f, nullptr, 0};
+  p.seq = (int)seq;
+  p.batch = (int)batch;
+  p.valid_lens = valid_lens;
+  p.scale_log2 = scale * 1.4426950408889634f;
+  launch_qkv_attn(p, as_stream(stream));
+  return check_launch(who);
 }
 
 // Shape / operand checks shared by the int8 entry points.

@@ -6,6 +6,10 @@ One post-LN layer is seven launches, in the reference encoder's order
   1. QKV GEMM + bias            x[M,H] . Wqkv[3H,H]^T         -> qkv[M,3H]
   2. flash attention            reads Q/K/V straight out of qkv by stride
                                 (no split/transpose kernels), writes ctx[M,H]
+     For sequences of 64 or 128 tokens and head_dim 64, steps 1-2 are one
+     launch (zk_qkv_attn_f16): each 256 x 192 GEMM tile is one head of whole
+     sequences and runs their attention in its epilogue, so Q, K and V never
+     reach HBM (six launches per layer).
   3. out-proj GEMM + bias       ctx . Wo^T                    -> t[M,H]
   4. Add+LayerNorm              LN(t + x)                     -> h1[M,H]
   5. FFN-up GEMM + bias + GELU  h1 . Wi^T                     -> u[M,4H]
@@ -60,7 +64,8 @@ class BertEncoder:
     """
 
     def __init__(self, layers: list[dict], heads: int = 12, eps: float = 1e-12,
-                 gelu: str = "erf", device: str | torch.device = "cuda"):
+                 gelu: str = "erf", device: str | torch.device = "cuda",
+                 fuse_qkv_attention: bool = True):
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise RuntimeError("BertEncoder runs on a GPU device")
@@ -73,12 +78,16 @@ class BertEncoder:
         if self.hidden % heads:
             raise RuntimeError("hidden size must be a multiple of heads")
         self.head_dim = self.hidden // heads
+        self.fuse_qkv_attention = bool(fuse_qkv_attention)
         d = self.device
         self.layers = []
         for w in layers:
+            # Q, K, V weights interleaved per head (q_h, k_h, v_h): one GEMM
+            # tile of 3 * head_dim columns is one head, for the fused kernel;
+            # the unfused attention reads the same layout by stride.
             self.layers.append({
-                "Wqkv": _dev(np.concatenate([w["Wq"], w["Wk"], w["Wv"]], 0), F16, d),
-                "bqkv": _dev(np.concatenate([w["bq"], w["bk"], w["bv"]], 0), F16, d),
+                "Wqkv": _dev(self._per_head(w["Wq"], w["Wk"], w["Wv"]), F16, d),
+                "bqkv": _dev(self._per_head(w["bq"], w["bk"], w["bv"]), F16, d),
                 "Wo": _dev(w["Wo"], F16, d), "bo": _dev(w["bo"], F16, d),
                 "ln1_g": _dev(w["ln1_g"], F16, d), "ln1_b": _dev(w["ln1_b"], F16, d),
                 "Wi": _dev(w["Wi"], F16, d), "bi": _dev(w["bi"], F16, d),
@@ -88,6 +97,18 @@ class BertEncoder:
         self.int8 = None
         self._bufs = None
         self._graph = None
+
+    def _per_head(self, q: np.ndarray, k: np.ndarray, v: np.ndarray) -> np.ndarray:
+        D = self.head_dim
+        parts = []
+        for h in range(self.heads):
+            parts += [q[h * D:(h + 1) * D], k[h * D:(h + 1) * D], v[h * D:(h + 1) * D]]
+        return np.concatenate(parts, 0)
+
+    def fused_attention(self, S: int) -> bool:
+        """Whether sequences of S tokens take the fused QKV + attention
+        launch (zk_qkv_attn_f16: S of 64 or 128, head_dim 64)."""
+        return self.fuse_qkv_attention and S in (64, 128) and self.head_dim == 64
 
     # ------------------------------------------------------------ INT8 FFN --
     def enable_int8_ffn(self, s_x: list[float], s_h: list[float], layers_fp32: list[dict] | None = None):
@@ -150,14 +171,22 @@ class BertEncoder:
         H, D, nh = self.hidden, self.head_dim, self.heads
         M = B * S
         qkv, ctx, t, h1, u = bf["qkv"], bf["ctx"], bf["t"], bf["h1"], bf["u"]
-        self._gemm(x, w["Wqkv"], w["bqkv"], qkv, L.ZK_EPI_BIAS, stream=stream)
-        base = qkv.data_ptr()
-        es = qkv.element_size()
-        ld = 3 * H
-        strides = L.strides_arg([S * ld, D, ld, S * ld, D, ld, S * ld, D, ld, S * H, D, H])
-        L.call("zk_flash_attn_fwd", base, base + H * es, base + 2 * H * es, ctx.data_ptr(),
-               B, nh, S, S, D, strides, None if lens is None else lens.data_ptr(),
-               float(1.0 / np.sqrt(D)), L.ZK_F16, stream)
+        scale = float(1.0 / np.sqrt(D))
+        if self.fused_attention(S):
+            L.call("zk_qkv_attn_f16", x.data_ptr(), w["Wqkv"].data_ptr(), w["bqkv"].data_ptr(),
+                   ctx.data_ptr(), B, S, H, nh, None if lens is None else lens.data_ptr(),
+                   scale, stream)
+        else:
+            self._gemm(x, w["Wqkv"], w["bqkv"], qkv, L.ZK_EPI_BIAS, stream=stream)
+            # per-head q, k, v column blocks: head h at columns 3 D h + (0, D, 2 D)
+            base = qkv.data_ptr()
+            es = qkv.element_size()
+            ld = 3 * H
+            strides = L.strides_arg([S * ld, 3 * D, ld, S * ld, 3 * D, ld, S * ld, 3 * D, ld,
+                                     S * H, D, H])
+            L.call("zk_flash_attn_fwd", base, base + D * es, base + 2 * D * es, ctx.data_ptr(),
+                   B, nh, S, S, D, strides, None if lens is None else lens.data_ptr(),
+                   scale, L.ZK_F16, stream)
         self._gemm(ctx, w["Wo"], w["bo"], t, L.ZK_EPI_BIAS, stream=stream)
         if self.int8 is None:
             L.call("zk_layernorm", t.data_ptr(), x.data_ptr(), w["ln1_g"].data_ptr(),
