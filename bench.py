@@ -10,9 +10,10 @@ replayed from a HIP graph, inputs resident in HBM. Prints ONE JSON line with:
                        same fp16 encoder at seq 512, config 5's other
                        length, in `encoder_s512`)
   roofline             the dominant kernel of the timed step: the longest of
-                       the kernels one encoder layer launches (fused QKV
-                       projection + attention, out-projection, Add+LN,
-                       FFN-up, FFN-down), as measured
+                       the four kernels one encoder layer launches (fused
+                       QKV projection + attention, out-projection, FFN-up,
+                       FFN-down, with the LayerNorms folded into them), as
+                       measured
                        in the `kernels` table (HIP events on the launch
                        stream); `traffic` from its rocprofv3 FETCH_SIZE /
                        WRITE_SIZE summary profiles/hbm_traffic_pmc.md
@@ -212,6 +213,73 @@ def kernel_cases(torch, dev):
                 f"B={B} S={S} heads={heads} M={B * S} K={H} N={3 * H} + attention (dense FLOPs)"
         return setup
 
+    def res_stats(M, K, N, ln_res=True):
+        """The encoder's out-projection / FFN-down with the folded LayerNorm:
+        bias + residual (LayerNorm-ed on the fly) + row statistics."""
+        def setup():
+            a = torch.from_numpy(synthetic.uniform((M, K), tag=1)).to(dev, f16)
+            w = torch.from_numpy(synthetic.uniform((N, K), tag=2)).to(dev, f16) * 0.05
+            b = torch.zeros(N, dtype=f16, device=dev)
+            r = torch.from_numpy(synthetic.normal((M, N), tag=3)).to(dev, f16)
+            c = torch.empty((M, N), dtype=f16, device=dev)
+            ms = torch.zeros((M, 2), dtype=torch.float32, device=dev)
+            ms[:, 1] = 1.0
+            g = torch.ones(N, dtype=f16, device=dev)
+            be = torch.zeros(N, dtype=f16, device=dev)
+            part = torch.empty((M, N // 96, 2), dtype=torch.float32, device=dev)
+            keep = (a, w, b, r, c, ms, g, be, part)
+            args = (a.data_ptr(), w.data_ptr(), c.data_ptr(), M, N, K, K, K, N, b.data_ptr(),
+                    r.data_ptr(), N, ms.data_ptr() if ln_res else None,
+                    g.data_ptr() if ln_res else None, be.data_ptr() if ln_res else None,
+                    part.data_ptr())
+            return (lambda i: _rc(L, lib.zk_gemm_f16_res_stats(*args, s())) and keep), \
+                2.0 * M * N * K, "TFLOP/s", "fp16", "mfma", \
+                f"M={M} K={K} N={N} + residual LayerNorm + row statistics"
+        return setup
+
+    def gemm_ln(M, K, N, gelu):
+        """The encoder's FFN-up with the folded LayerNorm of its input."""
+        def setup():
+            a = torch.from_numpy(synthetic.normal((M, K), tag=1)).to(dev, f16)
+            w = torch.from_numpy(synthetic.uniform((N, K), tag=2)).to(dev, f16) * 0.05
+            part = torch.zeros((M, K // 96, 2), dtype=torch.float32, device=dev)
+            part[..., 1] = 96.0
+            sc = torch.zeros(N, dtype=torch.float32, device=dev)
+            cc = torch.zeros(N, dtype=torch.float32, device=dev)
+            c = torch.empty((M, N), dtype=f16, device=dev)
+            mr = torch.empty((M, 2), dtype=torch.float32, device=dev)
+            keep = (a, w, part, sc, cc, c, mr)
+            args = (a.data_ptr(), w.data_ptr(), c.data_ptr(), M, N, K, K, K, N, part.data_ptr(),
+                    1e-12, sc.data_ptr(), cc.data_ptr(), mr.data_ptr(),
+                    L.ZK_EPI_BIAS_GELU_ERF if gelu else L.ZK_EPI_BIAS)
+            return (lambda i: _rc(L, lib.zk_gemm_f16_ln(*args, s())) and keep), \
+                2.0 * M * N * K, "TFLOP/s", "fp16", "mfma", \
+                f"M={M} K={K} N={N} on LayerNorm-ed rows (folded)" + (" + GELU" if gelu else "")
+        return setup
+
+    def qkv_attn_ln(B=32, S=128, heads=12):
+        """The encoder's fused QKV projection + attention with the previous
+        layer's LayerNorm folded in (layers 2-12 at s128)."""
+        def setup():
+            H = heads * 64
+            x = torch.from_numpy(synthetic.normal((B * S, H), tag=70)).to(dev, f16)
+            w = torch.from_numpy(synthetic.normal((3 * H, H), tag=71, std=0.05)).to(dev, f16)
+            part = torch.zeros((B * S, H // 96, 2), dtype=torch.float32, device=dev)
+            part[..., 1] = 96.0
+            sc = torch.zeros(3 * H, dtype=torch.float32, device=dev)
+            cc = torch.zeros(3 * H, dtype=torch.float32, device=dev)
+            mr = torch.empty((B * S, 2), dtype=torch.float32, device=dev)
+            ctx = torch.empty((B * S, H), dtype=f16, device=dev)
+            lens = torch.from_numpy(synthetic.padding_lengths(B, S)).to(dev)
+            keep = (x, w, part, sc, cc, mr, ctx, lens)
+            args = (x.data_ptr(), w.data_ptr(), part.data_ptr(), 1e-12, sc.data_ptr(),
+                    cc.data_ptr(), mr.data_ptr(), ctx.data_ptr(), B, S, H, heads,
+                    lens.data_ptr(), 1.0 / math.sqrt(64))
+            return (lambda i: _rc(L, lib.zk_qkv_attn_f16_ln(*args, s())) and keep), \
+                2.0 * B * S * 3 * H * H + 4.0 * B * heads * S * S * 64, "TFLOP/s", "fp16", "mfma", \
+                f"B={B} S={S} heads={heads} + attention (dense FLOPs), LayerNorm folded"
+        return setup
+
     def add_ln(M=4096):
         def setup():
             H = 768
@@ -296,6 +364,11 @@ def kernel_cases(torch, dev):
         "gemm_sq8192": gemm(8192, 8192, 8192, L.ZK_EPI_NONE),
         "attn_s128": attn(128),
         "qkv_attn_s128": qkv_attn(),
+        # the four launches of an encoder layer at b32 s128 (LayerNorms folded)
+        "qkv_attn_ln_s128": qkv_attn_ln(),
+        "out_proj_res_stats": res_stats(4096, 768, 768),
+        "ffn_up_ln": gemm_ln(4096, 768, 3072, True),
+        "ffn_down_res_stats": res_stats(4096, 3072, 768),
         "attn_s512": attn(512),
         "int8_ffn_up": gemm_i8(4096, 768, 3072, L.ZK_EPI_BIAS_GELU_ERF, requant=True),
         "int8_ffn_down": gemm_i8(4096, 3072, 768, E),
@@ -314,8 +387,7 @@ def kernel_cases(torch, dev):
 
 # kernels one step of the timed encoder (b32 s128) launches, per layer: the
 # roofline line names the longest of them
-STEP_KERNELS = ("qkv_attn_s128", "gemm_out_proj", "add_layernorm", "gemm_ffn_up",
-                "gemm_ffn_down")
+STEP_KERNELS = ("qkv_attn_ln_s128", "out_proj_res_stats", "ffn_up_ln", "ffn_down_res_stats")
 KERNEL_DESC = {
     "gemm_qkv": "gemm_mfma_kernel<F16Op, bias> M=4096 K=768 N=2304 (QKV)",
     "gemm_out_proj": "gemm_mfma_kernel<F16Op, bias> M=4096 K=768 N=768 (out-projection)",
@@ -324,6 +396,13 @@ KERNEL_DESC = {
     "attn_s128": "fa_fwd_f16_q16_kernel B=32 H=12 S=128 D=64, key padding",
     "qkv_attn_s128": "gemm_mfma_kernel<F16Op, QKV + attention epilogue> M=4096 K=768 N=2304 "
                      "+ attention B=32 H=12 S=128 D=64 (fused QKV projection and attention)",
+    "qkv_attn_ln_s128": "gemm_mfma_kernel<F16Op, QKV + attention epilogue, folded LayerNorm> "
+                        "M=4096 K=768 N=2304 + attention B=32 H=12 S=128 D=64",
+    "out_proj_res_stats": "gemm_mfma_kernel<F16Op, bias + LayerNorm-ed residual + row statistics> "
+                          "M=4096 K=768 N=768 (out-projection)",
+    "ffn_up_ln": "gemm_mfma_kernel<F16Op, folded LayerNorm + erf-GELU> M=4096 K=768 N=3072 (FFN-up)",
+    "ffn_down_res_stats": "gemm_mfma_kernel<F16Op, bias + LayerNorm-ed residual + row statistics> "
+                          "M=4096 K=3072 N=768 (FFN-down)",
     "add_layernorm": "ln_wave_kernel fp16 [4096,768] with residual",
 }
 

@@ -163,6 +163,55 @@ int zk_qkv_attn_f16(const void *X, const void *Wqkv, const void *bqkv, void *ctx
                     int64_t batch, int64_t seq, int64_t hidden, int64_t heads,
                     const int32_t *valid_lens, float scale, void *stream);
 
+/* The same with the LayerNorm of X's rows folded in: X holds the LN input
+ * x, Wqkv is gamma-scaled (W'[n,k] = W[n,k] gamma[k], rows interleaved per
+ * head as above), and q, k, v = rstd (x . W'^T - mean ln_s) + ln_c with
+ * ln_s[n] = sum_k W'[n,k] and ln_c = beta . W^T + bias (fp32 [3H], 16-byte
+ * aligned). The row statistics come from ln_part [B*S][H/96][2]: (mean, M2)
+ * of every 96-column segment of the row (as zk_gemm_f16_res_stats writes
+ * them), merged in a fixed order; (mean, rstd) of every row go to ln_out
+ * [B*S][2] when it is not NULL. H a multiple of 96, at most 1536;
+ * statistics arrays 8-byte aligned. No reference counterpart: the LayerNorm
+ * before the QKV projection (the previous reference layer's final one,
+ * benchmarks/bert_fp16_full.py:142-143, layernorm_fp16_gpu) folded into it. */
+int zk_qkv_attn_f16_ln(const void *X, const void *Wqkv, const float *ln_part, float ln_eps,
+                       const float *ln_s, const float *ln_c, float *ln_out, void *ctx,
+                       int64_t batch, int64_t seq, int64_t hidden, int64_t heads,
+                       const int32_t *valid_lens, float scale, void *stream);
+
+/* fp16 GEMM with a residual and the row statistics of its output:
+ *   C = A[M,K] . W[N,K]^T + bias + R,  R = res, or with res_ln [M][2]
+ *       (mean, rstd per row): R = (res - mean) rstd gamma + beta
+ *   part_out [M][N/96][2] = (mean, M2) of each 96-column segment of each
+ *       row of C as stored (fp16-rounded values)
+ * N a multiple of 96; K, lda, ldw, ldc, ldr multiples of 8; A, W, C, res,
+ * gamma, beta 16-byte aligned; res_ln and part_out 8-byte aligned. With
+ * res_ln it is the reference's residual add of a LayerNorm output
+ * (benchmarks/bert_fp16_full.py:128-130, 141-143: add_fp16_gpu of the
+ * previous layernorm_fp16_gpu result) with that LayerNorm computed on the
+ * fly; the statistics let the next GEMM fold the following LayerNorm
+ * (zk_gemm_f16_ln). No single reference counterpart. */
+int zk_gemm_f16_res_stats(const void *A, const void *W, void *C, int64_t M, int64_t N,
+                          int64_t K, int64_t lda, int64_t ldw, int64_t ldc,
+                          const void *bias, const void *res, int64_t ldr, const float *res_ln,
+                          const void *res_gamma, const void *res_beta, float *part_out,
+                          void *stream);
+
+/* fp16 GEMM on LayerNorm-ed rows, the LayerNorm folded into the weights:
+ *   C = act(rstd (A . W'^T - mean ln_s) + ln_c)
+ * A holds the LN input; W' = gamma-scaled weights (W'[n,k] = W[n,k]
+ * gamma[k]), ln_s[n] = sum_k W'[n,k], ln_c = beta . W^T + bias (fp32 [N],
+ * 16-byte aligned); per-row statistics from ln_part [M][K/96][2] as for
+ * zk_qkv_attn_f16_ln, (mean, rstd) written to ln_out [M][2] if not NULL.
+ * K a multiple of 96, at most 1536; epilogue ZK_EPI_BIAS (no activation) or
+ * ZK_EPI_BIAS_GELU_ERF. Replaces layernorm_fp16_gpu + linear_fp16_gpu +
+ * gelu_fp16_gpu of the reference layer (benchmarks/bert_fp16_full.py:
+ * 129-134). */
+int zk_gemm_f16_ln(const void *A, const void *W, void *C, int64_t M, int64_t N, int64_t K,
+                   int64_t lda, int64_t ldw, int64_t ldc, const float *ln_part, float ln_eps,
+                   const float *ln_s, const float *ln_c, float *ln_out, int epilogue,
+                   void *stream);
+
 /* Flash-attention forward, non-causal, online softmax with fp32 statistics.
  *   O[b,h,s,:] = softmax(scale * Q[b,h,s,:] . K[b,h,:,:]^T) . V[b,h,:,:]
  * Tensors are addressed by strides (elements): strides[0..2] are the

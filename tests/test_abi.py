@@ -78,6 +78,29 @@ def test_library_exports_every_declared_symbol():
      L.ZK_ERR_INVALID),
     (lambda lib: lib.zk_qkv_attn_f16(16, 16, 16, 12, 2, 128, 768, 12, None, 0.125, None),
      L.ZK_ERR_UNSUPPORTED),  # ctx not 8-byte aligned
+    (lambda lib: lib.zk_gemm_f16_res_stats(16, 16, 16, 8, 64, 64, 64, 64, 64, 16, 16, 64, None,
+                                           None, None, 16, None),
+     L.ZK_ERR_UNSUPPORTED),  # N not a multiple of the 96-column statistics segment
+    (lambda lib: lib.zk_gemm_f16_res_stats(16, 16, 16, 8, 96, 64, 64, 64, 96, 16, 16, 96, 16,
+                                           None, None, 16, None),
+     L.ZK_ERR_INVALID),  # residual LayerNorm without gamma / beta
+    (lambda lib: lib.zk_gemm_f16_res_stats(16, 16, 16, 8, 96, 64, 64, 64, 96, 16, 16, 96, None,
+                                           None, None, None, None),
+     L.ZK_ERR_INVALID),  # no statistics output
+    (lambda lib: lib.zk_gemm_f16_ln(16, 16, 16, 8, 64, 96, 96, 96, 64, 16, 1e-12, 16, 16, None,
+                                    L.ZK_EPI_BIAS_RELU, None), L.ZK_ERR_UNSUPPORTED),
+    (lambda lib: lib.zk_gemm_f16_ln(16, 16, 16, 8, 64, 64, 64, 64, 64, 16, 1e-12, 16, 16, None,
+                                    L.ZK_EPI_BIAS, None), L.ZK_ERR_UNSUPPORTED),  # K % 96
+    (lambda lib: lib.zk_gemm_f16_ln(16, 16, 16, 8, 64, 1632, 1632, 1632, 64, 16, 1e-12, 16, 16,
+                                    None, L.ZK_EPI_BIAS, None), L.ZK_ERR_UNSUPPORTED),  # K > 1536
+    (lambda lib: lib.zk_gemm_f16_ln(16, 16, 16, 8, 64, 96, 96, 96, 64, None, 1e-12, 16, 16, None,
+                                    L.ZK_EPI_BIAS, None), L.ZK_ERR_INVALID),
+    (lambda lib: lib.zk_gemm_f16_ln(16, 16, 16, 8, 64, 96, 96, 96, 64, 16, -1.0, 16, 16, None,
+                                    L.ZK_EPI_BIAS, None), L.ZK_ERR_INVALID),
+    (lambda lib: lib.zk_qkv_attn_f16_ln(16, 16, None, 1e-12, 16, 16, None, 16, 2, 128, 768, 12,
+                                        None, 0.125, None), L.ZK_ERR_INVALID),
+    (lambda lib: lib.zk_qkv_attn_f16_ln(16, 16, 16, 1e-12, None, 16, None, 16, 2, 128, 768, 12,
+                                        None, 0.125, None), L.ZK_ERR_INVALID),
     (lambda lib: lib.zk_layernorm_add(16, None, 16, 16, 16, 4, 8, 1e-5, L.ZK_F32, None),
      L.ZK_ERR_INVALID),  # LayerNormAdd needs its residual
     (lambda lib: lib.zk_layernorm_add(16, 16, 16, 16, 16, 4, 8, 1e-5, L.ZK_I8, None),

@@ -34,21 +34,24 @@ def test_config1_single_layer(dev):
     _check(y, obert.bert_encoder(x, w))
 
 
-@pytest.mark.parametrize("S,fused", [(128, True), (128, False), (512, False)])
-def test_config5_encoder_fp16(dev, S, fused):
+@pytest.mark.parametrize("S,fused,fold", [(128, True, True), (128, False, True),
+                                          (128, True, False), (512, False, True),
+                                          (512, False, False)])
+def test_config5_encoder_fp16(dev, S, fused, fold):
     """12 layers, B=32, lengths ~ U{S/2..S}, against the fp32 oracle: every
     sequence at S=128, with the fused QKV + attention launch (the default at
-    S=128) and with the separate GEMM and attention kernels; at S=512 eight
-    sequences spread over the batch (the full batch is covered bit-exactly by
-    the permutation test below)."""
+    S=128) and with the separate GEMM and attention kernels, with the
+    LayerNorms folded into the GEMMs (the default) and as separate kernels;
+    at S=512 eight sequences spread over the batch (the full batch is covered
+    bit-exactly by the permutation test below)."""
     from zenith_amd.encoder import BertEncoder
 
     B = 32
     w = _r16(synthetic.bert_weights(12, seed=42))
     x = synthetic.round_f16(synthetic.hidden_states(B, S, seed=42))
     lens = synthetic.padding_lengths(B, S)
-    enc = BertEncoder(w, device=dev, fuse_qkv_attention=fused)
-    assert enc.fused_attention(S) == fused
+    enc = BertEncoder(w, device=dev, fuse_qkv_attention=fused, fold_layernorm=fold)
+    assert enc.fused_attention(S) == fused and enc.fold_ln == fold
     y = enc(torch.from_numpy(x).to(dev, torch.float16), torch.from_numpy(lens).to(dev)).float().cpu().numpy()
     assert np.isfinite(y).all()
     pick = np.arange(B) if S == 128 else np.array([0, 5, 9, 14, 18, 23, 27, 31])

@@ -52,6 +52,12 @@ SIGNATURES: dict[str, list] = {
     "zk_linear_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _i32,
                       _vp, _i64, _vp],
     "zk_qkv_attn_f16": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _f32, _vp],
+    "zk_qkv_attn_f16_ln": [_vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp,
+                           _f32, _vp],
+    "zk_gemm_f16_res_stats": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64,
+                              _vp, _vp, _vp, _vp, _vp],
+    "zk_gemm_f16_ln": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _f32, _vp, _vp,
+                       _vp, _i32, _vp],
     "zk_flash_attn_fwd": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                           ctypes.POINTER(_i64), _vp, _f32, _i32, _vp],
     "zk_flash_attn_fwd_masked": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,

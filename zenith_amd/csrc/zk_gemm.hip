@@ -72,11 +72,65 @@ struct GemmParams {
   int batch;
   const int32_t *valid_lens;
   float scale_log2;
+  // LayerNorm of the A rows folded into the GEMM (kEpiLnIn*, and the fused
+  // attention when ln_part is set): A holds the LN input x, the weight is
+  // gamma-scaled (W'[n,k] = W[n,k] gamma[k]) and the epilogue forms
+  //   rstd[m] (acc - mean[m] ln_s[n]) + ln_c[n],
+  // ln_s = column sums of W', ln_c = beta . W^T + bias. mean / rstd come from
+  // the per-row partial statistics ln_part [M][ln_nparts] of (mean, M2) over
+  // kLnSeg-column segments; tile column 0 writes them to ln_out [M] if set.
+  const float *ln_part;
+  int ln_nparts;
+  float ln_eps;
+  const float *ln_s;
+  const float *ln_c;
+  float *ln_out;
+  // kEpiResStats: the residual is LN(res) with res_ln [M] (mean, rstd) and
+  // fp16 res_gamma / res_beta when res_ln is set; the fp16-rounded outputs'
+  // per-row (mean, M2) over kLnSeg-column segments go to part_out
+  // [M][N / kLnSeg].
+  const float *res_ln;
+  const void *res_gamma;
+  const void *res_beta;
+  float *part_out;
 };
 
-// Epilogue of the fused QKV projection + attention (internal; not one of the
-// public ZK_EPI_* values).
+// Internal epilogues (not public ZK_EPI_* values): the fused QKV projection +
+// attention; bias + residual (optionally LayerNorm-ed on the fly) with
+// per-row partial statistics of the output; and the folded LayerNorm of the
+// input rows, without or with erf-GELU.
 constexpr int kEpiQkvAttn = 100;
+constexpr int kEpiResStats = 101;
+constexpr int kEpiLnIn = 102;
+constexpr int kEpiLnInGelu = 103;
+
+// Row statistics travel as (mean, M2) partials of kLnSeg-column segments
+// (the 96-column wave tiles of the producing GEMM); a consumer holds at most
+// kLnMaxParts of them per row in registers (rows of up to 1536 values).
+constexpr int kLnSeg = 96;
+constexpr int kLnMaxParts = 16;
+
+// (mean, rstd) of a row of nparts x kLnSeg values from its partial
+// (mean, M2) pairs (Chan et al.'s pairwise update for equal counts, in a
+// fixed order).
+__device__ __forceinline__ float2 ln_merge(const float2 (&pr)[kLnMaxParts], int nparts,
+                                           float eps) {
+  float sm = 0.f;
+#pragma unroll
+  for (int q = 0; q < kLnMaxParts; ++q)
+    if (q < nparts) sm += pr[q].x;
+  const float mean = sm / (float)nparts;
+  float m2 = 0.f, dev = 0.f;
+#pragma unroll
+  for (int q = 0; q < kLnMaxParts; ++q)
+    if (q < nparts) {
+      const float d = pr[q].x - mean;
+      m2 += pr[q].y;
+      dev = fmaf(d, d, dev);
+    }
+  const float var = fmaf((float)kLnSeg, dev, m2) / ((float)kLnSeg * (float)nparts);
+  return make_float2(mean, 1.0f / sqrtf(var + eps));
+}
 
 // MFMA step on 16 bytes per lane and operand. MS = 32: lane l supplies row
 // l % 32, bytes [16 * (l / 32), +16) of the 32-byte k-step; the result
@@ -267,6 +321,39 @@ void gemm_mfma_kernel(GemmParams p) {
   }
   tile_of(twg, nwg, p, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
+  // Folded LayerNorm: the partial statistics of row m0 + tid are loaded
+  // into registers here, so that the loads overlap the main loop; they are
+  // merged after it.
+  constexpr bool LN_ROWS = EPI == kEpiLnIn || EPI == kEpiLnInGelu || EPI == kEpiQkvAttn;
+  static_assert(BM <= 64 * WM * WN, "one thread per tile row");
+  float2 ln_pr[LN_ROWS ? kLnMaxParts : 1];
+  if constexpr (LN_ROWS) {
+    const bool mine = p.ln_part && (int)threadIdx.x < BM && m0 + (int)threadIdx.x < p.M;
+    const float2 *src = (const float2 *)p.ln_part + (int64_t)(m0 + threadIdx.x) * p.ln_nparts;
+#pragma unroll
+    for (int q = 0; q < kLnMaxParts; ++q)
+      ln_pr[q] = mine && q < p.ln_nparts ? src[q] : make_float2(0.f, 0.f);
+  }
+  // kEpiResStats on 4-wave tiles (one 32-row stripe per wave): the
+  // residual rows of the wave's stripe (and their LayerNorm statistics) are
+  // loaded into registers here, under the main loop, instead of in one burst
+  // at the end.
+  constexpr bool RES_PREF = EPI == kEpiResStats && G::TM == 1 && WM * WN == 4 &&
+                            std::is_same<OutT, f16>::value;
+  constexpr int NPV = RES_PREF ? (MS * (WTN / 8) + 63) / 64 : 1;
+  f16x8 res_pv[NPV];
+  float2 res_ms[NPV];
+  if constexpr (RES_PREF) {
+#pragma unroll
+    for (int k = 0; k < NPV; ++k) {
+      const int v = lane + 64 * k, rl = v / (WTN / 8), cl = (v % (WTN / 8)) * 8;
+      const int row = m0 + wm * WTM + rl, col = n0 + wn * WTN + cl;
+      const bool in = v < MS * (WTN / 8) && row < p.M && col + 8 <= p.N;
+      res_pv[k] = in ? *(const f16x8 *)((const f16 *)p.res + (int64_t)row * p.ldr + col)
+                     : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      res_ms[k] = in && p.res_ln ? ((const float2 *)p.res_ln)[row] : make_float2(0.f, 0.f);
+    }
+  }
   const int kbytes = p.K * OP::kElem;
   const int64_t lda_b = p.lda * OP::kElem, ldb_b = p.ldb * OP::kElem;
   const int a_rows = min(BM, p.M - m0), b_rows = min(BN, p.N - n0);
@@ -408,19 +495,42 @@ void gemm_mfma_kernel(GemmParams p) {
     f16 *qkv = (f16 *)smem;  // 3 x 256 x 64 halves = 96 KB, inside the ring
     const f16 *bias = (const f16 *)p.bias;
     const int h32 = lane >> 5;
+    // With ln_part the rows of X are the LayerNorm input: Q, K, V are
+    // rstd (acc - mean s) + c (see GemmParams), (mean, rstd) per row in LDS.
+    float2 *lnt = (float2 *)(smem + 3 * BM * HD * 2);
+    static_assert(3 * BM * HD * 2 + BM * 8 <= G::SMEM, "LN table does not fit");
+    const bool ln = p.ln_part != nullptr;
+    if (ln) {
+      if ((int)threadIdx.x < BM) {
+        const float2 ms = ln_merge(ln_pr, p.ln_nparts, p.ln_eps);
+        lnt[threadIdx.x] = ms;
+        if (p.ln_out && tn == 0 && m0 + (int)threadIdx.x < p.M)
+          ((float2 *)p.ln_out)[m0 + threadIdx.x] = ms;
+      }
+      __syncthreads();
+    }
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int cb = wn * WTN + j * 32;  // first tile column of the block
-      const int d = cb % HD + (lane & 31);
-      const float bv = to_f(bias[n0 + cb + (lane & 31)]);
-      f16 *dst = qkv + (cb / HD) * (BM * HD);
+    for (int i = 0; i < TM; ++i) {
+      float2 ms[16];
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+      for (int r = 0; r < 16; ++r)
+        ms[r] = ln ? lnt[wm * WTM + i * 32 + 8 * (r >> 2) + 4 * h32 + (r & 3)]
+                   : make_float2(0.f, 1.f);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int cb = wn * WTN + j * 32;  // first tile column of the block
+        const int d = cb % HD + (lane & 31), n = n0 + cb + (lane & 31);
+        const float sv = ln ? p.ln_s[n] : 0.f;
+        const float cv = ln ? p.ln_c[n] : to_f(bias[n]);
+        f16 *dst = qkv + (cb / HD) * (BM * HD);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int row = wm * WTM + i * 32 + 8 * (r >> 2) + 4 * h32 + (r & 3);
-          dst[row * HD + (((d >> 3) ^ kv_swz(row)) << 3) + (d & 7)] = (f16)(acc[i][j][r] + bv);
+          const float v = ln ? fmaf(ms[r].y, fmaf(-ms[r].x, sv, acc[i][j][r]), cv)
+                             : acc[i][j][r] + cv;
+          dst[row * HD + (((d >> 3) ^ kv_swz(row)) << 3) + (d & 7)] = (f16)v;
         }
+      }
     }
     __syncthreads();
     // Wave w owns the 32 queries of tile rows [32 w, 32 w + 32); their
@@ -462,9 +572,23 @@ void gemm_mfma_kernel(GemmParams p) {
       }
     }
   } else {
-
     // Epilogue: per wave, one MS-row stripe at a time.
+    constexpr bool RES_STATS = EPI == kEpiResStats;
+    constexpr bool LN_IN = EPI == kEpiLnIn || EPI == kEpiLnInGelu;
+    constexpr bool RESID = EPI == ZK_EPI_BIAS_RESIDUAL || RES_STATS;
     float *ws = (float *)smem + wave * MS * G::EPITCH;
+    // LN_IN: (mean, rstd) of the tile's rows, in LDS beyond the stripes
+    float2 *lnt = (float2 *)(smem + G::EPI_BYTES);
+    if constexpr (LN_IN) {
+      static_assert(G::EPI_BYTES + BM * 8 <= G::SMEM, "LN table does not fit");
+      if ((int)threadIdx.x < BM) {
+        const float2 ms = ln_merge(ln_pr, p.ln_nparts, p.ln_eps);
+        lnt[threadIdx.x] = ms;
+        if (p.ln_out && tn == 0 && m0 + (int)threadIdx.x < p.M)
+          ((float2 *)p.ln_out)[m0 + threadIdx.x] = ms;
+      }
+      __syncthreads();
+    }
     // int8 output (re-quantisation): bias and residual are fp16; the value is
     // rounded to fp16 first, so the result equals quantising the fp16 output.
     constexpr bool Q8 = std::is_same<OutT, int8_t>::value;
@@ -474,41 +598,67 @@ void gemm_mfma_kernel(GemmParams p) {
     const BiasT *res = (const BiasT *)p.res;
     const float inv_q = Q8 ? 1.0f / p.s_q : 1.0f;
     const bool vec_ok = (p.ldc % 8 == 0) && (Q8 ? aligned8(p.C) : aligned16(p.C)) &&
-                        (EPI != ZK_EPI_BIAS_RESIDUAL || ((p.ldr % 8 == 0) && aligned16(p.res)));
+                        (!RESID || ((p.ldr % 8 == 0) && aligned16(p.res)));
     float bj[TN], sj[TN];
-  #pragma unroll
+#pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int col = n0 + wn * WTN + j * MS + frow;
       bj[j] = 0.f;
       sj[j] = 1.f;
       if (col < p.N) {
-        if (EPI != ZK_EPI_NONE) bj[j] = to_f(bias[col]);
+        if (EPI != ZK_EPI_NONE && !LN_IN) bj[j] = to_f(bias[col]);
         if (DEQ) sj[j] = p.s_x * p.s_w[col];
+        if (LN_IN) {  // column sum of W' and offset for this lane's column
+          sj[j] = p.ln_s[col];
+          bj[j] = p.ln_c[col];
+        }
       }
     }
+    // the residual's value at (row, col) (RES_STATS with res_ln: its LayerNorm)
+    auto resid = [&](int row, int col, float r) {
+      if constexpr (RES_STATS) {
+        if (p.res_ln) {
+          const float2 ms = ((const float2 *)p.res_ln)[row];
+          return fmaf((r - ms.x) * ms.y, to_f(((const f16 *)p.res_gamma)[col]),
+                      to_f(((const f16 *)p.res_beta)[col]));
+        }
+      }
+      return r;
+    };
     constexpr int VPR = WTN / 8;  // 8-column vectors per stripe row
-  #pragma unroll
+#pragma unroll
     for (int i = 0; i < TM; ++i) {
-  #pragma unroll
+      // LN_IN: (mean, rstd) of the rows this lane's registers hold
+      float2 msr[LN_IN ? R : 1];
+      if constexpr (LN_IN) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          msr[r] = lnt[wm * WTM + i * MS + (MS == 32 ? 8 * (r >> 2) + 4 * fch + (r & 3) : 4 * fch + r)];
+      }
+#pragma unroll
       for (int j = 0; j < TN; ++j) {
-  #pragma unroll
+#pragma unroll
         for (int r = 0; r < R; ++r) {
           const int rl = MS == 32 ? 8 * (r >> 2) + 4 * fch + (r & 3) : 4 * fch + r;
           float *dst = ws + rl * G::EPITCH + j * MS + frow;
           if constexpr (std::is_same<OutT, int32_t>::value) {
             *(int *)dst = acc[i][j][r];
+          } else if constexpr (LN_IN) {
+            // rstd (acc - mean s) + c, then the activation
+            const float t = fmaf(msr[r].y, fmaf(-msr[r].x, sj[j], (float)acc[i][j][r]), bj[j]);
+            *dst = EPI == kEpiLnInGelu ? gelu_erf_fast(t) : t;
           } else {
             const float v = DEQ ? (float)acc[i][j][r] * sj[j] : (float)acc[i][j][r];
-            *dst = epilogue<EPI>(v, bj[j]);
+            *dst = epilogue<RES_STATS ? (int)ZK_EPI_BIAS : EPI>(v, bj[j]);
           }
         }
       }
       const int row0 = m0 + wm * WTM + i * MS, col0 = n0 + wn * WTN;
-      for (int v = lane; v < MS * VPR; v += 64) {
+      auto store_vec = [&](int v, int k) {
         const int rl = v / VPR, cl = (v % VPR) * 8;
         const int row = row0 + rl, col = col0 + cl;
-        if (row >= p.M || col >= p.N) continue;
-        const float *src = ws + rl * G::EPITCH + cl;
+        if (row >= p.M || col >= p.N) return;
+        float *src = ws + rl * G::EPITCH + cl;
         OutT *dst = C + (int64_t)row * p.ldc + col;
         if (vec_ok && col + 8 <= p.N) {
           const f32x4 lo = *(const f32x4 *)src, hi = *(const f32x4 *)(src + 4);
@@ -517,25 +667,39 @@ void gemm_mfma_kernel(GemmParams p) {
             *(f32x4 *)(dst + 4) = hi;
           } else {
             float o[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            if constexpr (EPI == ZK_EPI_BIAS_RESIDUAL) {
+            if constexpr (RESID) {
               const BiasT *rp = res + (int64_t)row * p.ldr + col;
               if constexpr (std::is_same<BiasT, f16>::value) {
-                const f16x8 rv = *(const f16x8 *)rp;
-  #pragma unroll
-                for (int e = 0; e < 8; ++e) o[e] += (float)rv[e];
+                const f16x8 rv = RES_PREF ? res_pv[k] : *(const f16x8 *)rp;
+                if (RES_STATS && p.res_ln) {
+                  // LN(res): one (mean, rstd) per row, gamma / beta as vectors
+                  const float2 ms = RES_PREF ? res_ms[k] : ((const float2 *)p.res_ln)[row];
+                  const f16x8 g = *(const f16x8 *)((const f16 *)p.res_gamma + col);
+                  const f16x8 bb = *(const f16x8 *)((const f16 *)p.res_beta + col);
+#pragma unroll
+                  for (int e = 0; e < 8; ++e)
+                    o[e] += fmaf(((float)rv[e] - ms.x) * ms.y, (float)g[e], (float)bb[e]);
+                } else {
+#pragma unroll
+                  for (int e = 0; e < 8; ++e) o[e] += (float)rv[e];
+                }
               } else {
-  #pragma unroll
-                for (int e = 0; e < 8; ++e) o[e] += to_f(rp[e]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] += resid(row, col + e, to_f(rp[e]));
               }
             }
             if constexpr (std::is_same<OutT, f16>::value) {
               f16x8 h;
-  #pragma unroll
+#pragma unroll
               for (int e = 0; e < 8; ++e) h[e] = (f16)o[e];
               store_nt((f16x8 *)dst, h);
+              if constexpr (RES_STATS) {  // the stored values, for the statistics
+                *(f32x4 *)src = f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+                *(f32x4 *)(src + 4) = f32x4{(float)h[4], (float)h[5], (float)h[6], (float)h[7]};
+              }
             } else if constexpr (Q8) {
               uint32_t qlo = 0, qhi = 0;
-  #pragma unroll
+#pragma unroll
               for (int e = 0; e < 4; ++e) {
                 qlo |= (uint32_t)(uint8_t)quant1((float)(f16)o[e], p.s_q, inv_q) << (8 * e);
                 qhi |= (uint32_t)(uint8_t)quant1((float)(f16)o[e + 4], p.s_q, inv_q) << (8 * e);
@@ -552,11 +716,50 @@ void gemm_mfma_kernel(GemmParams p) {
               dst[e] = ((const int *)src)[e];
             } else {
               float o = src[e];
-              if (EPI == ZK_EPI_BIAS_RESIDUAL) o += to_f(res[(int64_t)row * p.ldr + col + e]);
+              if (RESID) o += resid(row, col + e, to_f(res[(int64_t)row * p.ldr + col + e]));
               if constexpr (Q8) dst[e] = quant1((float)(f16)o, p.s_q, inv_q);
               else dst[e] = (OutT)o;
+              if constexpr (RES_STATS) src[e] = (float)(OutT)o;
             }
           }
+        }
+      };
+      if constexpr (RES_PREF) {
+#pragma unroll
+        for (int k = 0; k < NPV; ++k)
+          if (lane + 64 * k < MS * VPR) store_vec(lane + 64 * k, k);
+      } else {
+        for (int v = lane; v < MS * VPR; v += 64) store_vec(v, 0);
+      }
+      if constexpr (RES_STATS) {
+        // (mean, M2) of every kLnSeg-column segment of the stripe's rows,
+        // from the stored (rounded) values; one lane per (row, segment)
+        static_assert(WTN % kLnSeg == 0, "statistics segments");
+        constexpr int SEG = WTN / kLnSeg;
+        for (int v = lane; v < MS * SEG; v += 64) {
+          const int rl = v / SEG, sg = v % SEG;
+          const int row = row0 + rl;
+          if (row >= p.M || col0 + kLnSeg * sg >= p.N) continue;
+          const f32x4 *x4 = (const f32x4 *)(ws + rl * G::EPITCH + kLnSeg * sg);
+          float sum = 0.f;
+#pragma unroll
+          for (int q = 0; q < kLnSeg / 4; ++q) {
+            const f32x4 t = x4[q];
+            sum += (t[0] + t[1]) + (t[2] + t[3]);
+          }
+          const float mean = sum * (1.0f / kLnSeg);
+          float m2 = 0.f;
+#pragma unroll
+          for (int q = 0; q < kLnSeg / 4; ++q) {
+            const f32x4 t = x4[q];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float d = t[e] - mean;
+              m2 = fmaf(d, d, m2);
+            }
+          }
+          ((float2 *)p.part_out)[(int64_t)row * (p.N / kLnSeg) + col0 / kLnSeg + sg] =
+              make_float2(mean, m2);
         }
       }
     }
@@ -599,6 +802,16 @@ static void launch_epi(GemmParams p, int epi, hipStream_t s) {
       if constexpr (!std::is_same<OutT, int8_t>::value) ZK_L(ZK_EPI_BIAS_RESIDUAL);
       break;
     case ZK_EPI_BIAS_RELU: ZK_L(ZK_EPI_BIAS_RELU); break;
+    default:
+      // the folded-LayerNorm epilogues: fp16 in and out only; statistics
+      // need wave tiles of whole 32-column segments
+      if constexpr (std::is_same<OP, F16Op>::value && std::is_same<OutT, f16>::value && !DEQ) {
+        if (epi == kEpiLnIn) ZK_L(kEpiLnIn);
+        if (epi == kEpiLnInGelu) ZK_L(kEpiLnInGelu);
+        if constexpr ((BN / WN) % kLnSeg == 0)
+          if (epi == kEpiResStats) ZK_L(kEpiResStats);
+      }
+      break;
   }
 #undef ZK_L
 }
@@ -894,14 +1107,23 @@ static void launch_qkv_attn(GemmParams p, hipStream_t s) {
       <<<grid, 512, 0, s>>>(p);
 }
 
-extern "C" int zk_qkv_attn_f16(const void *X, const void *Wqkv, const void *bqkv, void *ctx,
-                               int64_t batch, int64_t seq, int64_t hidden, int64_t heads,
-                               const int32_t *valid_lens, float scale, void *stream) {
-  const char *who = "zk_qkv_attn_f16";
+static int qkv_attn_impl(const char *who, const void *X, const void *Wqkv, const void *bqkv,
+                         const float *ln_part, float ln_eps, const float *ln_s,
+                         const float *ln_c, float *ln_out, void *ctx, int64_t batch,
+                         int64_t seq, int64_t hidden, int64_t heads, const int32_t *valid_lens,
+                         float scale, void *stream) {
   if (batch < 0 || seq <= 0 || hidden <= 0 || heads <= 0)
     return fail(ZK_ERR_INVALID, "%s: bad size", who);
   if (batch == 0) return ZK_OK;
-  if (!X || !Wqkv || !bqkv || !ctx) return fail(ZK_ERR_INVALID, "%s: null pointer", who);
+  if (!X || !Wqkv || !ctx) return fail(ZK_ERR_INVALID, "%s: null pointer", who);
+  if (!ln_part && !bqkv) return fail(ZK_ERR_INVALID, "%s: null bias", who);
+  if (ln_part && (!ln_s || !ln_c || !(ln_eps >= 0.f)))
+    return fail(ZK_ERR_INVALID, "%s: LayerNorm needs column sums, offsets and eps >= 0", who);
+  if (!aligned8(ln_part) || !aligned8(ln_out))
+    return fail(ZK_ERR_UNSUPPORTED, "%s: statistics arrays must be 8-byte aligned", who);
+  if (ln_part && (hidden % kLnSeg || hidden / kLnSeg > kLnMaxParts))
+    return fail(ZK_ERR_UNSUPPORTED, "%s: hidden must be a multiple of %d, at most %d", who,
+                kLnSeg, kLnSeg * kLnMaxParts);
   if (hidden != heads * 64)
     return fail(ZK_ERR_UNSUPPORTED, "%s: head dim must be 64 (hidden %lld, heads %lld)", who,
                 (long long)hidden, (long long)heads);
@@ -921,7 +1143,108 @@ extern "C" int zk_qkv_attn_f16(const void *X, const void *Wqkv, const void *bqkv
   p.batch = (int)batch;
   p.valid_lens = valid_lens;
   p.scale_log2 = scale * 1.4426950408889634f;
+  p.ln_part = ln_part;
+  p.ln_nparts = (int)(K / kLnSeg);
+  p.ln_eps = ln_eps;
+  p.ln_s = ln_s;
+  p.ln_c = ln_c;
+  p.ln_out = ln_out;
   launch_qkv_attn(p, as_stream(stream));
+  return check_launch(who);
+}
+
+extern "C" int zk_qkv_attn_f16(const void *X, const void *Wqkv, const void *bqkv, void *ctx,
+                               int64_t batch, int64_t seq, int64_t hidden, int64_t heads,
+                               const int32_t *valid_lens, float scale, void *stream) {
+  return qkv_attn_impl("zk_qkv_attn_f16", X, Wqkv, bqkv, nullptr, 0.f, nullptr, nullptr, nullptr,
+                       ctx, batch, seq, hidden, heads, valid_lens, scale, stream);
+}
+
+extern "C" int zk_qkv_attn_f16_ln(const void *X, const void *Wqkv, const float *ln_part,
+                                  float ln_eps, const float *ln_s, const float *ln_c,
+                                  float *ln_out, void *ctx, int64_t batch, int64_t seq,
+                                  int64_t hidden, int64_t heads, const int32_t *valid_lens,
+                                  float scale, void *stream) {
+  if (!ln_part) return fail(ZK_ERR_INVALID, "zk_qkv_attn_f16_ln: null statistics");
+  return qkv_attn_impl("zk_qkv_attn_f16_ln", X, Wqkv, nullptr, ln_part, ln_eps, ln_s, ln_c,
+                       ln_out, ctx, batch, seq, hidden, heads, valid_lens, scale, stream);
+}
+
+// Operand checks of the folded-LayerNorm GEMMs: fp16, W[N,K], dense-enough
+// rows in multiples of 8, 16-byte aligned.
+static int check_ln_gemm(const char *who, const void *A, const void *W, const void *C, int64_t M,
+                         int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc) {
+  int st = check_dims(who, M, N, K);
+  if (st) return st;
+  if (!A || !W || !C) return fail(ZK_ERR_INVALID, "%s: null pointer", who);
+  if (lda < K || ldw < K || ldc < N) return fail(ZK_ERR_INVALID, "%s: leading dimension too small", who);
+  if (K == 0 || K % 8 || lda % 8 || ldw % 8 || ldc % 8 || !aligned16(A) || !aligned16(W) ||
+      !aligned16(C))
+    return fail(ZK_ERR_UNSUPPORTED,
+                "%s: K and the leading dimensions must be multiples of 8, operands 16-byte "
+                "aligned", who);
+  return check_span(who, lda, ldw, K, 2);
+}
+
+extern "C" int zk_gemm_f16_res_stats(const void *A, const void *W, void *C, int64_t M, int64_t N,
+                                     int64_t K, int64_t lda, int64_t ldw, int64_t ldc,
+                                     const void *bias, const void *res, int64_t ldr,
+                                     const float *res_ln, const void *res_gamma,
+                                     const void *res_beta, float *part_out, void *stream) {
+  const char *who = "zk_gemm_f16_res_stats";
+  int st = check_ln_gemm(who, A, W, C, M, N, K, lda, ldw, ldc);
+  if (st) return st;
+  if (M == 0 || N == 0) return ZK_OK;
+  if (!bias || !res || !part_out) return fail(ZK_ERR_INVALID, "%s: null bias, residual or statistics", who);
+  if (N % kLnSeg)
+    return fail(ZK_ERR_UNSUPPORTED, "%s: N must be a multiple of %d", who, kLnSeg);
+  if (res_ln && (!res_gamma || !res_beta))
+    return fail(ZK_ERR_INVALID, "%s: residual LayerNorm needs gamma and beta", who);
+  if (ldr < N) return fail(ZK_ERR_INVALID, "%s: ldr < N", who);
+  if (ldr % 8 || !aligned16(res)) return fail(ZK_ERR_UNSUPPORTED, "%s: residual rows must be 16-byte aligned", who);
+  if (!aligned8(res_ln) || !aligned8(part_out) || !aligned16(res_gamma) || !aligned16(res_beta))
+    return fail(ZK_ERR_UNSUPPORTED,
+                "%s: statistics 8-byte, gamma and beta 16-byte aligned", who);
+  GemmParams p{A, W, C, (int)M, (int)N, (int)K, lda, ldw, ldc, bias, res, ldr, 1.f, nullptr, 0};
+  p.res_ln = res_ln;
+  p.res_gamma = res_gamma;
+  p.res_beta = res_beta;
+  p.part_out = part_out;
+  // the configurations whose wave tiles are one statistics segment wide:
+  // 256x192 (8 waves) once it fills the CUs, else 128x96 (4 waves)
+  const int64_t t192 = (M + 255) / 256 * (N / 192);
+  launch_mfma<F16Op, f16, false>(p, kEpiResStats, as_stream(stream),
+                                 M >= 1024 && N % 192 == 0 && t192 >= 160 ? 5 : 4);
+  return check_launch(who);
+}
+
+extern "C" int zk_gemm_f16_ln(const void *A, const void *W, void *C, int64_t M, int64_t N,
+                              int64_t K, int64_t lda, int64_t ldw, int64_t ldc,
+                              const float *ln_part, float ln_eps, const float *ln_s,
+                              const float *ln_c, float *ln_out, int epilogue, void *stream) {
+  const char *who = "zk_gemm_f16_ln";
+  int st = check_ln_gemm(who, A, W, C, M, N, K, lda, ldw, ldc);
+  if (st) return st;
+  if (M == 0 || N == 0) return ZK_OK;
+  if (!ln_part || !ln_s || !ln_c || !(ln_eps >= 0.f))
+    return fail(ZK_ERR_INVALID, "%s: null statistics, column sums or offsets, or eps < 0", who);
+  if (epilogue != ZK_EPI_BIAS && epilogue != ZK_EPI_BIAS_GELU_ERF)
+    return fail(ZK_ERR_UNSUPPORTED, "%s: epilogue must be ZK_EPI_BIAS or ZK_EPI_BIAS_GELU_ERF", who);
+  if (K % kLnSeg || K / kLnSeg > kLnMaxParts)
+    return fail(ZK_ERR_UNSUPPORTED, "%s: K must be a multiple of %d, at most %d", who, kLnSeg,
+                kLnSeg * kLnMaxParts);
+  if (!aligned8(ln_part) || !aligned8(ln_out) || !aligned16(ln_s) || !aligned16(ln_c))
+    return fail(ZK_ERR_UNSUPPORTED,
+                "%s: statistics 8-byte, column sums and offsets 16-byte aligned", who);
+  GemmParams p{A, W, C, (int)M, (int)N, (int)K, lda, ldw, ldc, nullptr, nullptr, 0, 1.f, nullptr, 0};
+  p.ln_part = ln_part;
+  p.ln_nparts = (int)(K / kLnSeg);
+  p.ln_eps = ln_eps;
+  p.ln_s = ln_s;
+  p.ln_c = ln_c;
+  p.ln_out = ln_out;
+  launch_mfma<F16Op, f16, false>(p, epilogue == ZK_EPI_BIAS ? kEpiLnIn : kEpiLnInGelu,
+                                 as_stream(stream));
   return check_launch(who);
 }
 

@@ -55,6 +55,19 @@ def quantize_weight_per_channel(w: torch.Tensor) -> tuple[torch.Tensor, torch.Te
     return q, s
 
 
+def fold_layernorm(w: np.ndarray, b: np.ndarray, gamma: np.ndarray, beta: np.ndarray):
+    """LayerNorm(x; gamma, beta) . w^T + b folded into the GEMM on x:
+    returns (w' as fp16-rounded float32 [N, K], s [N], c [N]) with
+    w'[n, k] = w[n, k] gamma[k], s = column sums of the rounded w', and
+    c = beta . w^T + b, so that LN(x) . w^T + b = rstd (x . w'^T - mean s) + c
+    (zk_gemm_f16_ln, zk_qkv_attn_f16_ln). w as stored (fp16-rounded)."""
+    w = np.asarray(w, np.float32)
+    wf = (w * np.asarray(gamma, np.float32)[None, :]).astype(np.float16).astype(np.float32)
+    s = wf.astype(np.float64).sum(1).astype(np.float32)
+    c = (w.astype(np.float64) @ np.asarray(beta, np.float64) + np.asarray(b, np.float64)).astype(np.float32)
+    return wf, s, c
+
+
 class BertEncoder:
     """12-layer (by default) BERT encoder resident on one GPU.
 
@@ -65,7 +78,7 @@ class BertEncoder:
 
     def __init__(self, layers: list[dict], heads: int = 12, eps: float = 1e-12,
                  gelu: str = "erf", device: str | torch.device = "cuda",
-                 fuse_qkv_attention: bool = True):
+                 fuse_qkv_attention: bool = True, fold_layernorm: bool = True):
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise RuntimeError("BertEncoder runs on a GPU device")
@@ -79,9 +92,14 @@ class BertEncoder:
             raise RuntimeError("hidden size must be a multiple of heads")
         self.head_dim = self.hidden // heads
         self.fuse_qkv_attention = bool(fuse_qkv_attention)
+        # LayerNorms folded into the GEMMs that consume them (fp16 FFN, erf
+        # GELU, hidden size a multiple of 96 up to 1536: the row statistics
+        # travel as (mean, M2) of 96-column segments)
+        self.fold_ln = (bool(fold_layernorm) and gelu == "erf" and self.hidden % 96 == 0
+                        and self.hidden <= 1536)
         d = self.device
         self.layers = []
-        for w in layers:
+        for i, w in enumerate(layers):
             # Q, K, V weights interleaved per head (q_h, k_h, v_h): one GEMM
             # tile of 3 * head_dim columns is one head, for the fused kernel;
             # the unfused attention reads the same layout by stride.
@@ -94,6 +112,8 @@ class BertEncoder:
                 "Wo2": _dev(w["Wo2"], F16, d), "bo2": _dev(w["bo2"], F16, d),
                 "ln2_g": _dev(w["ln2_g"], F16, d), "ln2_b": _dev(w["ln2_b"], F16, d),
             })
+            if self.fold_ln:
+                self.layers[-1].update(self._folded(w, layers[i - 1] if i > 0 else None))
         self.int8 = None
         self._bufs = None
         self._graph = None
@@ -104,6 +124,20 @@ class BertEncoder:
         for h in range(self.heads):
             parts += [q[h * D:(h + 1) * D], k[h * D:(h + 1) * D], v[h * D:(h + 1) * D]]
         return np.concatenate(parts, 0)
+
+    def _folded(self, w: dict, prev: dict | None) -> dict:
+        """LN1 folded into FFN-up, and the previous layer's LN2 into this
+        layer's QKV projection (weights, gamma and beta as stored in fp16)."""
+        d, r16 = self.device, (lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float32))
+        f32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(d)  # noqa: E731
+        wi, si, ci = fold_layernorm(r16(w["Wi"]), r16(w["bi"]), r16(w["ln1_g"]), r16(w["ln1_b"]))
+        out = {"Wi_f": _dev(wi, F16, d), "s_i": f32(si), "c_i": f32(ci)}
+        if prev is not None:
+            wq, sq, cq = fold_layernorm(r16(self._per_head(w["Wq"], w["Wk"], w["Wv"])),
+                                        r16(self._per_head(w["bq"], w["bk"], w["bv"])),
+                                        r16(prev["ln2_g"]), r16(prev["ln2_b"]))
+            out.update({"Wqkv_f": _dev(wq, F16, d), "s_qkv": f32(sq), "c_qkv": f32(cq)})
+        return out
 
     def fused_attention(self, S: int) -> bool:
         """Whether sequences of S tokens take the fused QKV + attention
@@ -153,6 +187,17 @@ class BertEncoder:
             "q_h": torch.empty((M, H), dtype=torch.int8, device=d),
             "q_u": torch.empty((M, I), dtype=torch.int8, device=d),
         }
+        if self.fold_ln:
+            f32 = torch.float32
+            self._bufs.update({
+                # partial (mean, M2) per 96-column segment of h and of h2
+                "p1": torch.empty((M, H // 96, 2), dtype=f32, device=d),
+                "p2a": torch.empty((M, H // 96, 2), dtype=f32, device=d),
+                "p2b": torch.empty((M, H // 96, 2), dtype=f32, device=d),
+                # (mean, rstd) per row of h (LN1) and of the layer input (LN2)
+                "mr1": torch.empty((M, 2), dtype=f32, device=d),
+                "mr2": torch.empty((M, 2), dtype=f32, device=d),
+            })
         self._graph = None
         return self._bufs
 
@@ -178,15 +223,7 @@ class BertEncoder:
                    scale, stream)
         else:
             self._gemm(x, w["Wqkv"], w["bqkv"], qkv, L.ZK_EPI_BIAS, stream=stream)
-            # per-head q, k, v column blocks: head h at columns 3 D h + (0, D, 2 D)
-            base = qkv.data_ptr()
-            es = qkv.element_size()
-            ld = 3 * H
-            strides = L.strides_arg([S * ld, 3 * D, ld, S * ld, 3 * D, ld, S * ld, 3 * D, ld,
-                                     S * H, D, H])
-            L.call("zk_flash_attn_fwd", base, base + D * es, base + 2 * D * es, ctx.data_ptr(),
-                   B, nh, S, S, D, strides, None if lens is None else lens.data_ptr(),
-                   scale, L.ZK_F16, stream)
+            self._attention(qkv, ctx, lens, B, S, stream)
         self._gemm(ctx, w["Wo"], w["bo"], t, L.ZK_EPI_BIAS, stream=stream)
         if self.int8 is None:
             L.call("zk_layernorm", t.data_ptr(), x.data_ptr(), w["ln1_g"].data_ptr(),
@@ -214,13 +251,88 @@ class BertEncoder:
              start: int = 0, stop: int | None = None):
         bf = self._bufs
         stream = torch.cuda.current_stream(self.device).cuda_stream
-        cur = x2
         stop = len(self.layers) if stop is None else stop
+        if self.fold_ln and self.int8 is None:
+            return self._run_folded(x2, lens, B, S, out, start, stop, stream)
+        cur = x2
         for i in range(start, stop):
             dst = out if i == stop - 1 else (bf["ping"] if i % 2 == 0 else bf["pong"])
             self._layer(i, cur, dst, lens, B, S, stream)
             cur = dst
         return out
+
+    def _run_folded(self, x2, lens, B, S, out, start, stop, stream):
+        """Layers [start, stop) with the LayerNorms folded into the GEMMs:
+        four launches per layer. Each layer keeps its output un-normalised
+        (h2 = FFN-down + residual) with per-row partial statistics; the next
+        layer's QKV projection applies LN2 through its folded weights and
+        its out-projection adds LN2(h2) as the residual on the fly; LN1 goes
+        the same way into FFN-up and FFN-down. One LayerNorm kernel at the
+        end materialises the last output."""
+        bf = self._bufs
+        H, D, nh, I = self.hidden, self.head_dim, self.heads, self.ffn
+        M, eps = B * S, self.eps
+        scale = float(1.0 / np.sqrt(D))
+        lp = None if lens is None else lens.data_ptr()
+        ctx, qkv, h, u = bf["ctx"], bf["qkv"], bf["h1"], bf["u"]
+        p1, mr1, mr2 = bf["p1"], bf["mr1"], bf["mr2"]
+        cur, cur_parts = x2, None  # layer input: materialised (first layer) or raw h2
+        for i in range(start, stop):
+            w = self.layers[i]
+            first = i == start
+            prev = None if first else self.layers[i - 1]
+            h2, p2 = (bf["ping"], bf["p2a"]) if i % 2 == 0 else (bf["pong"], bf["p2b"])
+            # 1-2. QKV projection (+ LN2 of the previous layer) and attention
+            if self.fused_attention(S):
+                if first:
+                    L.call("zk_qkv_attn_f16", cur.data_ptr(), w["Wqkv"].data_ptr(),
+                           w["bqkv"].data_ptr(), ctx.data_ptr(), B, S, H, nh, lp, scale, stream)
+                else:
+                    L.call("zk_qkv_attn_f16_ln", cur.data_ptr(), w["Wqkv_f"].data_ptr(),
+                           cur_parts.data_ptr(), self.eps, w["s_qkv"].data_ptr(),
+                           w["c_qkv"].data_ptr(), mr2.data_ptr(), ctx.data_ptr(), B, S, H, nh,
+                           lp, scale, stream)
+            else:
+                if first:
+                    self._gemm(cur, w["Wqkv"], w["bqkv"], qkv, L.ZK_EPI_BIAS, stream=stream)
+                else:
+                    L.call("zk_gemm_f16_ln", cur.data_ptr(), w["Wqkv_f"].data_ptr(), qkv.data_ptr(),
+                           M, 3 * H, H, H, H, 3 * H, cur_parts.data_ptr(), self.eps,
+                           w["s_qkv"].data_ptr(), w["c_qkv"].data_ptr(), mr2.data_ptr(),
+                           L.ZK_EPI_BIAS, stream)
+                self._attention(qkv, ctx, lens, B, S, stream)
+            # 3. out-projection + residual (the input, or LN2(input)) -> h, stats
+            L.call("zk_gemm_f16_res_stats", ctx.data_ptr(), w["Wo"].data_ptr(), h.data_ptr(),
+                   M, H, H, H, H, H, w["bo"].data_ptr(), cur.data_ptr(), H,
+                   None if first else mr2.data_ptr(),
+                   None if first else prev["ln2_g"].data_ptr(),
+                   None if first else prev["ln2_b"].data_ptr(), p1.data_ptr(), stream)
+            # 4. FFN-up on LN1(h) + GELU
+            L.call("zk_gemm_f16_ln", h.data_ptr(), w["Wi_f"].data_ptr(), u.data_ptr(), M, I, H, H,
+                   H, I, p1.data_ptr(), self.eps, w["s_i"].data_ptr(), w["c_i"].data_ptr(),
+                   mr1.data_ptr(), L.ZK_EPI_BIAS_GELU_ERF, stream)
+            # 5. FFN-down + LN1(h) -> h2, stats
+            L.call("zk_gemm_f16_res_stats", u.data_ptr(), w["Wo2"].data_ptr(), h2.data_ptr(),
+                   M, H, I, I, I, H, w["bo2"].data_ptr(), h.data_ptr(), H, mr1.data_ptr(),
+                   w["ln1_g"].data_ptr(), w["ln1_b"].data_ptr(), p2.data_ptr(), stream)
+            cur, cur_parts = h2, p2
+        w = self.layers[stop - 1]
+        L.call("zk_layernorm", cur.data_ptr(), None, w["ln2_g"].data_ptr(), w["ln2_b"].data_ptr(),
+               out.data_ptr(), M, H, self.eps, L.ZK_F16, stream)
+        return out
+
+    def _attention(self, qkv, ctx, lens, B, S, stream):
+        """Attention over the per-head q, k, v column blocks of qkv (head h
+        at columns 3 D h + (0, D, 2 D))."""
+        H, D, nh = self.hidden, self.head_dim, self.heads
+        base = qkv.data_ptr()
+        es = qkv.element_size()
+        ld = 3 * H
+        strides = L.strides_arg([S * ld, 3 * D, ld, S * ld, 3 * D, ld, S * ld, 3 * D, ld,
+                                 S * H, D, H])
+        L.call("zk_flash_attn_fwd", base, base + D * es, base + 2 * D * es, ctx.data_ptr(),
+               B, nh, S, S, D, strides, None if lens is None else lens.data_ptr(),
+               float(1.0 / np.sqrt(D)), L.ZK_F16, stream)
 
     def _check(self, x: torch.Tensor, lens):
         if x.dim() != 3 or x.shape[-1] != self.hidden:
