@@ -133,15 +133,16 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
-// Wait until at most min(allowed, N) slices of PER instructions each are
-// still in flight (allowed is wave-uniform).
-template <int N, int PER>
+// Wait until at most min(allowed, N) slices of PER instructions each, plus
+// EXTRA loads issued after them, are still in flight (allowed is
+// wave-uniform).
+template <int N, int PER, int EXTRA = 0>
 __device__ __forceinline__ void wait_slices(int allowed) {
   if constexpr (N == 0) {
-    wait_vmcnt<0>();
+    wait_vmcnt<EXTRA>();
   } else {
-    if (allowed >= N) wait_vmcnt<N * PER>();
-    else wait_slices<N - 1, PER>(allowed);
+    if (allowed >= N) wait_vmcnt<N * PER + EXTRA>();
+    else wait_slices<N - 1, PER, EXTRA>(allowed);
   }
 }
 // Workgroup barrier without the fence __syncthreads() carries: the fence

@@ -334,26 +334,33 @@ void gemm_mfma_kernel(GemmParams p) {
     for (int q = 0; q < kLnMaxParts; ++q)
       ln_pr[q] = mine && q < p.ln_nparts ? src[q] : make_float2(0.f, 0.f);
   }
-  // kEpiResStats on 4-wave tiles (one 32-row stripe per wave): the
-  // residual rows of the wave's stripe (and their LayerNorm statistics) are
-  // loaded into registers here, under the main loop, instead of in one burst
-  // at the end.
-  constexpr bool RES_PREF = EPI == kEpiResStats && G::TM == 1 && WM * WN == 4 &&
-                            std::is_same<OutT, f16>::value;
-  constexpr int NPV = RES_PREF ? (MS * (WTN / 8) + 63) / 64 : 1;
-  f16x8 res_pv[NPV];
-  float2 res_ms[NPV];
-  if constexpr (RES_PREF) {
+  // kEpiResStats: the residual rows of the wave's first stripe (and their
+  // LayerNorm statistics) are loaded into registers under the main loop,
+  // issued right after the first slices; those of its other stripes right
+  // after the main loop, all at once, instead of one dependent load per
+  // vector in the epilogue. Every lane loads (out-of-range lanes from the
+  // first element), so a stripe is exactly NRL vector loads, which the
+  // slice waits that see them in flight count.
+  constexpr int NPV0 = (MS * (WTN / 8) + 63) / 64;
+  constexpr bool RES_PREF = EPI == kEpiResStats && std::is_same<OutT, f16>::value && NPV0 <= 6;
+  constexpr int NPV = RES_PREF ? NPV0 : 1, NPT = RES_PREF ? G::TM : 1;
+  constexpr int NRL = RES_PREF ? 2 * NPV : 0;
+  f16x8 res_pv[NPT][NPV];
+  float2 res_ms[NPT][NPV];
+  auto load_res = [&](int i) {
+    const f16 *rb = (const f16 *)p.res;
+    const float2 *lb = p.res_ln ? (const float2 *)p.res_ln : (const float2 *)p.res;
 #pragma unroll
     for (int k = 0; k < NPV; ++k) {
       const int v = lane + 64 * k, rl = v / (WTN / 8), cl = (v % (WTN / 8)) * 8;
-      const int row = m0 + wm * WTM + rl, col = n0 + wn * WTN + cl;
+      const int row = m0 + wm * WTM + i * MS + rl, col = n0 + wn * WTN + cl;
       const bool in = v < MS * (WTN / 8) && row < p.M && col + 8 <= p.N;
-      res_pv[k] = in ? *(const f16x8 *)((const f16 *)p.res + (int64_t)row * p.ldr + col)
-                     : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      res_ms[k] = in && p.res_ln ? ((const float2 *)p.res_ln)[row] : make_float2(0.f, 0.f);
+      // kept whatever `in` is (the epilogue reads only in-range vectors, and
+      // res_ms only with res_ln), so that no lane's load is predicated away
+      res_pv[i][k] = *(const f16x8 *)(rb + (in ? (int64_t)row * p.ldr + col : 0));
+      res_ms[i][k] = lb[in && p.res_ln ? row : 0];
     }
-  }
+  };
   const int kbytes = p.K * OP::kElem;
   const int64_t lda_b = p.lda * OP::kElem, ldb_b = p.ldb * OP::kElem;
   const int a_rows = min(BM, p.M - m0), b_rows = min(BN, p.N - n0);
@@ -450,7 +457,15 @@ void gemm_mfma_kernel(GemmParams p) {
 #pragma unroll
     for (int s = 0; s < ST; ++s)
       if (s < nk) ZK_ISSUE(s, s);
-    wait_slices<ST - 1, IA + IB>(nk - 1);
+    // the residual loads follow the prologue slices (the empty asm keeps the
+    // compiler from moving them ahead): the waits for slices 0 .. ST - 1 let
+    // these NRL younger loads stay in flight
+    if constexpr (RES_PREF) {
+      asm volatile("" ::: "memory");
+      load_res(0);
+      asm volatile("" ::: "memory");
+    }
+    wait_slices<ST - 1, IA + IB, NRL>(nk - 1);
     lds_barrier();
     rd(0, 0, 0);
     // Main loop over slices. Before the last k-step of slice kt every wave
@@ -470,7 +485,8 @@ void gemm_mfma_kernel(GemmParams p) {
     for (int kt = 0; kt + 1 < nk; ++kt) {
       steps_but_last(stage);
       const int next = stage + 1 == ST ? 0 : stage + 1;
-      wait_slices<ST - 2, IA + IB>(nk - 2 - kt);
+      if (NRL > 0 && kt + 1 < ST) wait_slices<ST - 2, IA + IB, NRL>(nk - 2 - kt);
+      else wait_slices<ST - 2, IA + IB>(nk - 2 - kt);
       lds_barrier();
       if (kt + ST < nk) ZK_ISSUE(kt + ST, stage);
       rd(next, 0, 0);
@@ -482,6 +498,24 @@ void gemm_mfma_kernel(GemmParams p) {
     mma_step(1);
   }
 #undef ZK_ISSUE
+  // With res_ln, the residual LayerNorm's gamma and beta at this lane's
+  // vector columns (the same for every stripe of the wave), loaded together
+  // before any epilogue store: a load issued after a store could only be
+  // waited for together with that store.
+  f16x8 res_g[NPV], res_b[NPV];
+  if constexpr (RES_PREF) {
+#pragma unroll
+    for (int i = 1; i < NPT; ++i) load_res(i);
+    if (p.res_ln) {
+#pragma unroll
+      for (int k = 0; k < NPV; ++k) {
+        const int col = n0 + wn * WTN + ((lane + 64 * k) % (WTN / 8)) * 8;
+        const int64_t c = col + 8 <= p.N ? col : 0;
+        res_g[k] = *(const f16x8 *)((const f16 *)p.res_gamma + c);
+        res_b[k] = *(const f16x8 *)((const f16 *)p.res_beta + c);
+      }
+    }
+  }
   __syncthreads();  // every wave is done reading the ring; it becomes epilogue space
   if constexpr (EPI == kEpiQkvAttn) {
     // The tile is the Q, K and V columns of head tn (weights interleaved
@@ -670,12 +704,13 @@ void gemm_mfma_kernel(GemmParams p) {
             if constexpr (RESID) {
               const BiasT *rp = res + (int64_t)row * p.ldr + col;
               if constexpr (std::is_same<BiasT, f16>::value) {
-                const f16x8 rv = RES_PREF ? res_pv[k] : *(const f16x8 *)rp;
+                const f16x8 rv = RES_PREF ? res_pv[RES_PREF ? i : 0][k] : *(const f16x8 *)rp;
                 if (RES_STATS && p.res_ln) {
                   // LN(res): one (mean, rstd) per row, gamma / beta as vectors
-                  const float2 ms = RES_PREF ? res_ms[k] : ((const float2 *)p.res_ln)[row];
-                  const f16x8 g = *(const f16x8 *)((const f16 *)p.res_gamma + col);
-                  const f16x8 bb = *(const f16x8 *)((const f16 *)p.res_beta + col);
+                  const float2 ms = RES_PREF ? res_ms[RES_PREF ? i : 0][k]
+                                             : ((const float2 *)p.res_ln)[row];
+                  const f16x8 g = RES_PREF ? res_g[k] : *(const f16x8 *)((const f16 *)p.res_gamma + col);
+                  const f16x8 bb = RES_PREF ? res_b[k] : *(const f16x8 *)((const f16 *)p.res_beta + col);
 #pragma unroll
                   for (int e = 0; e < 8; ++e)
                     o[e] += fmaf(((float)rv[e] - ms.x) * ms.y, (float)g[e], (float)bb[e]);
@@ -733,33 +768,42 @@ void gemm_mfma_kernel(GemmParams p) {
       }
       if constexpr (RES_STATS) {
         // (mean, M2) of every kLnSeg-column segment of the stripe's rows,
-        // from the stored (rounded) values; one lane per (row, segment)
-        static_assert(WTN % kLnSeg == 0, "statistics segments");
-        constexpr int SEG = WTN / kLnSeg;
-        for (int v = lane; v < MS * SEG; v += 64) {
-          const int rl = v / SEG, sg = v % SEG;
+        // from the stored (rounded) values. Two neighbouring lanes per (row,
+        // segment), each over half of it; the halves are merged by Chan's
+        // rule: M2 = M2a + M2b + (mean_a - mean_b)^2 * n / 4.
+        static_assert(WTN % kLnSeg == 0 && kLnSeg % 8 == 0, "statistics segments");
+        constexpr int SEG = WTN / kLnSeg, HALF = kLnSeg / 2;
+        for (int v = lane; v < 2 * MS * SEG; v += 64) {  // 2 MS SEG is even: pairs stay together
+          const int pr = v >> 1, hf = v & 1;
+          const int rl = pr / SEG, sg = pr % SEG;
           const int row = row0 + rl;
-          if (row >= p.M || col0 + kLnSeg * sg >= p.N) continue;
-          const f32x4 *x4 = (const f32x4 *)(ws + rl * G::EPITCH + kLnSeg * sg);
-          float sum = 0.f;
+          const bool ok = row < p.M && col0 + kLnSeg * sg < p.N;
+          float mean = 0.f, m2 = 0.f;
+          if (ok) {
+            const f32x4 *x4 = (const f32x4 *)(ws + rl * G::EPITCH + kLnSeg * sg + HALF * hf);
+            float sum = 0.f;
 #pragma unroll
-          for (int q = 0; q < kLnSeg / 4; ++q) {
-            const f32x4 t = x4[q];
-            sum += (t[0] + t[1]) + (t[2] + t[3]);
-          }
-          const float mean = sum * (1.0f / kLnSeg);
-          float m2 = 0.f;
+            for (int q = 0; q < HALF / 4; ++q) {
+              const f32x4 t = x4[q];
+              sum += (t[0] + t[1]) + (t[2] + t[3]);
+            }
+            mean = sum * (1.0f / HALF);
 #pragma unroll
-          for (int q = 0; q < kLnSeg / 4; ++q) {
-            const f32x4 t = x4[q];
+            for (int q = 0; q < HALF / 4; ++q) {
+              const f32x4 t = x4[q];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float d = t[e] - mean;
-              m2 = fmaf(d, d, m2);
+              for (int e = 0; e < 4; ++e) {
+                const float d = t[e] - mean;
+                m2 = fmaf(d, d, m2);
+              }
             }
           }
-          ((float2 *)p.part_out)[(int64_t)row * (p.N / kLnSeg) + col0 / kLnSeg + sg] =
-              make_float2(mean, m2);
+          const float mo = __shfl_xor(mean, 1), m2o = __shfl_xor(m2, 1);
+          if (ok && hf == 0) {
+            const float d = mo - mean;
+            ((float2 *)p.part_out)[(int64_t)row * (p.N / kLnSeg) + col0 / kLnSeg + sg] =
+                make_float2(0.5f * (mean + mo), m2 + m2o + d * d * (0.25f * kLnSeg));
+          }
         }
       }
     }
