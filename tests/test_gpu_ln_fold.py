@@ -4,7 +4,9 @@
   LayerNorm from given per-row (mean, rstd)) against the fp32 oracle at the
   fp16 bar |y - ref| <= 2e-3 + 1e-2 |ref|; its per-row (mean, M2) of every
   96-column segment against the same statistics of the stored output,
-  computed in float64.
+  computed in float64. The shapes reach both tile configurations it uses,
+  128x96 with 4 x 1 waves and 256x192 with 8 waves (M >= 1024 filling the
+  CUs), at short and deep K and at ragged edges.
 - zk_gemm_f16_ln: act(LayerNorm(A) . W^T + b) from the partial statistics of
   A and the folded weights (encoder.fold_layernorm) against the oracle's
   LayerNorm, linear and GELU; the (mean, rstd) it writes against float64.
@@ -70,7 +72,8 @@ def _gamma_beta(K, tag):
 
 
 @pytest.mark.parametrize("M,K,N", [(4096, 768, 768), (4096, 3072, 768), (100, 64, 96),
-                                   (16384, 768, 768), (300, 256, 288), (2048, 768, 1536)])
+                                   (16384, 768, 768), (300, 256, 288), (2048, 768, 1536),
+                                   (300, 2304, 288), (100, 2048, 96), (16384, 3072, 768)])
 @pytest.mark.parametrize("ln_res", [False, True])
 def test_gemm_res_stats(dev, M, K, N, ln_res):
     a = synthetic.round_f16(synthetic.normal((M, K), tag=80))
