@@ -166,3 +166,18 @@ def test_quantize_near_ties(dev, scale):
     xh = x.astype(np.float16)
     qh = zc.quantize_int8(torch.from_numpy(xh).to(dev), float(s)).cpu().numpy()
     np.testing.assert_array_equal(qh, ops.quantize_int8(xh.astype(np.float32), s))
+
+
+def test_quantize_special_values(dev):
+    """Saturation, signed zero and non-finite inputs through the 8-wide
+    vector path (fp16 input) and the scalar path (fp32 input) alike: +-inf
+    and the largest fp16 values saturate, zeros give 0, NaN gives -128 (the
+    clamp returns its bound for NaN)."""
+    from zenith_amd import zenith_cuda as zc
+
+    v = np.array([np.nan, np.inf, -np.inf, 65504.0, -65504.0, 0.0, -0.0, 1.0], np.float32)
+    want = np.array([-128, 127, -128, 127, -128, 0, 0, 25], np.int8)
+    x = np.tile(v, 64)
+    for dt in (torch.float16, torch.float32):
+        q = zc.quantize_int8(torch.from_numpy(x).to(dev, dt), 0.04).cpu().numpy()
+        np.testing.assert_array_equal(q, np.tile(want, 64))

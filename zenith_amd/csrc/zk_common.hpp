@@ -71,6 +71,38 @@ __device__ __forceinline__ int8_t quant1(float x, float scale, float inv) {
   return (int8_t)(int)r;
 }
 
+// Eight values at once, the same result as quant1 on each, packed as int8.
+// t = RN(x * inv + 128) is one rounding of the exact x * inv + 128, so for
+// |x / scale| <= 128.5 it lies within 1.6e-5 + 7.7e-6 of x / scale + 128,
+// and within 3.1e-5 of RN(x / scale) + 128; rint(t) - 128 is therefore the
+// exact answer unless t lies within 6e-5 of a half-integer, and the group
+// takes the IEEE division when any of its eight does. Beyond 128.5 both
+// forms saturate. The offset makes every clamped value a byte in [0, 255]:
+// packed by v_cvt_pk_u8_f32 (exact on integers), then shifted back to
+// int8 by flipping each byte's top bit. The clamp is v_med3_f32, which
+// returns the minimum (0) when an operand is NaN: NaN gives -128, as in
+// quant1.
+__device__ __forceinline__ u32x2 quant8(const float (&x)[8], float scale, float inv) {
+  float r[8], dev = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float t = fmaf(x[e], inv, 128.0f);
+    r[e] = __builtin_rintf(t);
+    dev = fmaxf(dev, fabsf(t - r[e]));
+  }
+  if (dev >= 0.49994f) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = __builtin_rintf(x[e] / scale) + 128.0f;
+  }
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    lo = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_amdgcn_fmed3f(r[e], 0.f, 255.f), e, lo);
+    hi = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_amdgcn_fmed3f(r[e + 4], 0.f, 255.f), e, hi);
+  }
+  return u32x2{lo ^ 0x80808080u, hi ^ 0x80808080u};
+}
+
 // ------------------------------------------------------------ device math --
 __device__ __forceinline__ float gelu_erf(float x) {
   // 0.5 x (1 + erf(x / sqrt(2)))

@@ -185,13 +185,10 @@ __global__ void quant_f16_vec(const f16 *__restrict__ x, int8_t *__restrict__ q,
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nvec;
        i += stride) {
     f16x8 v = reinterpret_cast<const f16x8 *>(x)[i];
-    uint32_t lo = 0, hi = 0;
+    float vf[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      lo |= (uint32_t)(uint8_t)quant1((float)v[j], scale, inv) << (8 * j);
-      hi |= (uint32_t)(uint8_t)quant1((float)v[j + 4], scale, inv) << (8 * j);
-    }
-    store_nt(reinterpret_cast<u32x2 *>(q) + i, u32x2{lo, hi});
+    for (int j = 0; j < 8; ++j) vf[j] = (float)v[j];
+    store_nt(reinterpret_cast<u32x2 *>(q) + i, quant8(vf, scale, inv));
   }
 }
 

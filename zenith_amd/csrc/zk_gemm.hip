@@ -733,13 +733,10 @@ void gemm_mfma_kernel(GemmParams p) {
                 *(f32x4 *)(src + 4) = f32x4{(float)h[4], (float)h[5], (float)h[6], (float)h[7]};
               }
             } else if constexpr (Q8) {
-              uint32_t qlo = 0, qhi = 0;
+              float of[8];  // rounded to fp16 first: the fp16 output's quantisation
 #pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                qlo |= (uint32_t)(uint8_t)quant1((float)(f16)o[e], p.s_q, inv_q) << (8 * e);
-                qhi |= (uint32_t)(uint8_t)quant1((float)(f16)o[e + 4], p.s_q, inv_q) << (8 * e);
-              }
-              store_nt((u32x2 *)dst, u32x2{qlo, qhi});
+              for (int e = 0; e < 8; ++e) of[e] = (float)(f16)o[e];
+              store_nt((u32x2 *)dst, quant8(of, p.s_q, inv_q));
             } else {
               *(f32x4 *)dst = f32x4{o[0], o[1], o[2], o[3]};
               *(f32x4 *)(dst + 4) = f32x4{o[4], o[5], o[6], o[7]};

@@ -108,14 +108,10 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
       store_nt(yr + idx, o);
       if constexpr (Q8) {
         static_assert(W == 8, "int8 output is written 8 bytes per vector");
-        const float inv = 1.0f / qs;
-        uint32_t lo = 0, hi = 0;
+        float of[8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          lo |= (uint32_t)(uint8_t)quant1((float)o[j], qs, inv) << (8 * j);
-          hi |= (uint32_t)(uint8_t)quant1((float)o[j + 4], qs, inv) << (8 * j);
-        }
-        store_nt(reinterpret_cast<u32x2 *>(q + row * hidden) + idx, u32x2{lo, hi});
+        for (int j = 0; j < 8; ++j) of[j] = (float)o[j];
+        store_nt(reinterpret_cast<u32x2 *>(q + row * hidden) + idx, quant8(of, qs, 1.0f / qs));
       }
     }
   }
