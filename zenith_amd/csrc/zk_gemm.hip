@@ -323,7 +323,9 @@ void gemm_mfma_kernel(GemmParams p) {
   const int m0 = tm * BM, n0 = tn * BN;
   // Folded LayerNorm: the partial statistics of row m0 + tid are loaded
   // into registers here, so that the loads overlap the main loop; they are
-  // merged after it.
+  // merged after it. (Issued after the first slices instead, as the
+  // residual below is, they made the encoder 1% slower: a slice wait that
+  // does not count them holds until these loads return.)
   constexpr bool LN_ROWS = EPI == kEpiLnIn || EPI == kEpiLnInGelu || EPI == kEpiQkvAttn;
   static_assert(BM <= 64 * WM * WN, "one thread per tile row");
   float2 ln_pr[LN_ROWS ? kLnMaxParts : 1];
@@ -339,12 +341,13 @@ void gemm_mfma_kernel(GemmParams p) {
   // issued right after the first slices; those of its other stripes right
   // after the main loop, all at once, instead of one dependent load per
   // vector in the epilogue. Every lane loads (out-of-range lanes from the
-  // first element), so a stripe is exactly NRL vector loads, which the
+  // first element), so a stripe is exactly 2 NPV vector loads, which the
   // slice waits that see them in flight count.
   constexpr int NPV0 = (MS * (WTN / 8) + 63) / 64;
   constexpr bool RES_PREF = EPI == kEpiResStats && std::is_same<OutT, f16>::value && NPV0 <= 6;
   constexpr int NPV = RES_PREF ? NPV0 : 1, NPT = RES_PREF ? G::TM : 1;
-  constexpr int NRL = RES_PREF ? 2 * NPV : 0;
+  // loads issued right after the prologue slices, per wave
+  constexpr int NXL = RES_PREF ? 2 * NPV : 0;
   f16x8 res_pv[NPT][NPV];
   float2 res_ms[NPT][NPV];
   auto load_res = [&](int i) {
@@ -457,15 +460,15 @@ void gemm_mfma_kernel(GemmParams p) {
 #pragma unroll
     for (int s = 0; s < ST; ++s)
       if (s < nk) ZK_ISSUE(s, s);
-    // the residual loads follow the prologue slices (the empty asm keeps the
-    // compiler from moving them ahead): the waits for slices 0 .. ST - 1 let
-    // these NRL younger loads stay in flight
+    // the residual loads follow the prologue slices (the empty asm keeps
+    // the compiler from moving them ahead): the waits for slices 0 .. ST - 1
+    // let these NXL younger loads stay in flight
     if constexpr (RES_PREF) {
       asm volatile("" ::: "memory");
       load_res(0);
       asm volatile("" ::: "memory");
     }
-    wait_slices<ST - 1, IA + IB, NRL>(nk - 1);
+    wait_slices<ST - 1, IA + IB, NXL>(nk - 1);
     lds_barrier();
     rd(0, 0, 0);
     // Main loop over slices. Before the last k-step of slice kt every wave
@@ -485,7 +488,7 @@ void gemm_mfma_kernel(GemmParams p) {
     for (int kt = 0; kt + 1 < nk; ++kt) {
       steps_but_last(stage);
       const int next = stage + 1 == ST ? 0 : stage + 1;
-      if (NRL > 0 && kt + 1 < ST) wait_slices<ST - 2, IA + IB, NRL>(nk - 2 - kt);
+      if (NXL > 0 && kt + 1 < ST) wait_slices<ST - 2, IA + IB, NXL>(nk - 2 - kt);
       else wait_slices<ST - 2, IA + IB>(nk - 2 - kt);
       lds_barrier();
       if (kt + ST < nk) ZK_ISSUE(kt + ST, stage);
