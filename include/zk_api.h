@@ -112,6 +112,23 @@ int zk_layernorm_q8(const void *x, const void *residual, const void *gamma,
                     const void *beta, void *y, int8_t *q, int64_t rows,
                     int64_t hidden, float eps, float q_scale, void *stream);
 
+/* zk_layernorm_q8 whose residual is itself the LayerNorm of the given rows:
+ *   y = LN(x + LN'(residual); gamma, beta),  q = quant(y, q_scale)
+ *   LN'(r)[i, j] = (r[i, j] - mean_i) rstd_i res_gamma[j] + res_beta[j]
+ * with (mean_i, rstd_i) = res_ln [rows][2] (fp32, 8-byte aligned, as the
+ * LayerNorm-folded GEMMs write them), computed in fp32 without rounding
+ * LN'(r) to fp16. fp16 x, residual, gammas, betas and y. No single
+ * reference counterpart: the previous layer's closing Add+LayerNorm
+ * (layernorm_fp16_gpu, benchmarks/bert_fp16_full.py:141-143) left
+ * unmaterialised and applied where its output is the residual of this
+ * layer's Add+LayerNorm (:128-130, fused_add_layernorm
+ * fused_kernels.cu:145-221), followed by the int8 quantisation of the INT8
+ * FFN input (quantize_f32_to_int8_kernel cuda_kernels.cu:918-937). */
+int zk_layernorm_q8_res_ln(const void *x, const void *residual, const float *res_ln,
+                           const void *res_gamma, const void *res_beta, const void *gamma,
+                           const void *beta, void *y, int8_t *q, int64_t rows, int64_t hidden,
+                           float eps, float q_scale, void *stream);
+
 /* Out-of-place transpose of a [rows, cols] fp16 matrix (leading dim lds)
  * into [cols, rows] (leading dim ldd). Used to present B[K,N] as the
  * K-major operand the MFMA GEMM reads.
@@ -285,6 +302,23 @@ int zk_gemm_i8_requant(const int8_t *A, const int8_t *W, int8_t *Q, int64_t M,
                        int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldq,
                        float s_x, const float *s_w, const void *bias, int epilogue,
                        float s_out, void *stream);
+
+/* zk_gemm_f16_res_stats on the int8 product, dequantised as in zk_gemm_i8:
+ *   C = acc[m,n] * (s_x * s_w[n]) + bias[n] + R,  R = res, or with res_ln
+ *       its LayerNorm as in zk_gemm_f16_res_stats
+ *   part_out [M][N/96][2] = (mean, M2) of each 96-column segment of each row
+ *       of C as stored (fp16)
+ * fp16 C, bias, res (and res_gamma, res_beta); operand rules of zk_gemm_i8,
+ * N a multiple of 96, ldc and ldr multiples of 8, C and res 16-byte aligned.
+ * No single reference counterpart: the INT8 FFN-down (fused_int8_linear
+ * cuda_kernels.cu:1010-1049) with the residual add of the layer's closing
+ * Add+LayerNorm (benchmarks/bert_fp16_full.py:141-143) and the statistics
+ * that let the next layer fold that LayerNorm in. */
+int zk_gemm_i8_res_stats(const int8_t *A, const int8_t *W, void *C, int64_t M, int64_t N,
+                         int64_t K, int64_t lda, int64_t ldw, int64_t ldc, float s_x,
+                         const float *s_w, const void *bias, const void *res, int64_t ldr,
+                         const float *res_ln, const void *res_gamma, const void *res_beta,
+                         float *part_out, void *stream);
 
 /* c[r, :] = a[r, :] + b[b_rows == 1 ? 0 : r, :] for [rows, cols] contiguous
  * tensors in dtype ZK_F32 or ZK_F16 (fp16 summed in fp32, rounded once);

@@ -101,6 +101,24 @@ def test_library_exports_every_declared_symbol():
                                         None, 0.125, None), L.ZK_ERR_INVALID),
     (lambda lib: lib.zk_qkv_attn_f16_ln(16, 16, 16, 1e-12, None, 16, None, 16, 2, 128, 768, 12,
                                         None, 0.125, None), L.ZK_ERR_INVALID),
+    (lambda lib: lib.zk_gemm_i8_res_stats(16, 16, 16, 8, 64, 64, 64, 64, 64, 1.0, 16, 16, 16, 64,
+                                          None, None, None, 16, None),
+     L.ZK_ERR_UNSUPPORTED),  # N not a multiple of the 96-column statistics segment
+    (lambda lib: lib.zk_gemm_i8_res_stats(16, 16, 16, 8, 96, 64, 64, 64, 96, 1.0, None, 16, 16,
+                                          96, None, None, None, 16, None),
+     L.ZK_ERR_INVALID),  # no weight scales
+    (lambda lib: lib.zk_gemm_i8_res_stats(16, 16, 16, 8, 96, 72, 72, 72, 96, 1.0, 16, 16, 16, 96,
+                                          None, None, None, 16, None),
+     L.ZK_ERR_UNSUPPORTED),  # int8 K % 16
+    (lambda lib: lib.zk_gemm_i8_res_stats(16, 16, 16, 8, 96, 64, 64, 64, 96, 1.0, 16, 16, None,
+                                          96, None, None, None, 16, None),
+     L.ZK_ERR_INVALID),  # no residual
+    (lambda lib: lib.zk_layernorm_q8_res_ln(16, 16, None, 16, 16, 16, 16, 16, 16, 4, 8, 1e-12,
+                                            0.1, None), L.ZK_ERR_INVALID),  # no residual stats
+    (lambda lib: lib.zk_layernorm_q8_res_ln(16, 16, 16, 16, 16, 16, 16, 16, 16, 4, 8, 1e-12,
+                                            0.0, None), L.ZK_ERR_INVALID),  # q_scale
+    (lambda lib: lib.zk_layernorm_q8_res_ln(16, 16, 12, 16, 16, 16, 16, 16, 16, 4, 8, 1e-12,
+                                            0.1, None), L.ZK_ERR_UNSUPPORTED),  # res_ln alignment
     (lambda lib: lib.zk_layernorm_add(16, None, 16, 16, 16, 4, 8, 1e-5, L.ZK_F32, None),
      L.ZK_ERR_INVALID),  # LayerNormAdd needs its residual
     (lambda lib: lib.zk_layernorm_add(16, 16, 16, 16, 16, 4, 8, 1e-5, L.ZK_I8, None),

@@ -85,11 +85,14 @@ def test_config5_batch_permutation_invariance(dev, S, int8):
     assert torch.equal(yp, y[torch.from_numpy(perm).to(dev)])
 
 
-@pytest.mark.parametrize("S", [128, 512])
-def test_config5_encoder_int8_ffn(dev, S):
+@pytest.mark.parametrize("S,fold", [(128, True), (512, False), (128, False)])
+def test_config5_encoder_int8_ffn(dev, S, fold):
     """INT8-FFN variant at B=32, S=128 and S=512: per-layer activation scales
     calibrated on the oracle's fp32 activations; the oracle's INT8 encoder
-    uses the same scales and weight quantisation."""
+    uses the same scales and weight quantisation. With the LayerNorms folded
+    (LN2 into the next layer's QKV projection and LN1's residual, the int8
+    FFN-down writing h2 with its statistics; the default at S=128) and
+    unfolded (as the INT8-FFN encoder runs at S=512)."""
     from zenith_amd.encoder import BertEncoder
 
     B = 32
@@ -112,8 +115,9 @@ def test_config5_encoder_int8_ffn(dev, S):
         s_x.append(float(ops.absmax_scale(np.abs(h1).max())))
         s_h.append(float(ops.absmax_scale(np.abs(u).max())))
         h = obert.bert_layer(h, lw, lens[pick])
-    enc = BertEncoder(w, device=dev)
+    enc = BertEncoder(w, device=dev, fold_layernorm=fold)
     enc.enable_int8_ffn(s_x, s_h, layers_fp32=w)
+    assert enc.folded(S) == fold
     y = enc(torch.from_numpy(x).to(dev, torch.float16), torch.from_numpy(lens).to(dev)).float().cpu().numpy()
     int8_layers = []
     for i, lw in enumerate(w):

@@ -1,4 +1,4 @@
-"""GPU parity: the LayerNorm folded into the GEMMs (fp16).
+"""GPU parity: the LayerNorm folded into the GEMMs (fp16 and the INT8 FFN).
 
 - zk_gemm_f16_res_stats: C = A . W^T + bias + R (R = the residual, or its
   LayerNorm from given per-row (mean, rstd)) against the fp32 oracle at the
@@ -13,6 +13,10 @@
 - zk_qkv_attn_f16_ln: the fused QKV projection + attention on LayerNorm(X)
   against the oracle's LayerNorm, linear (rounded to fp16) and attention
   (norm-relative 1e-3, fp16 bar with 1.5x margin: see the test).
+- zk_gemm_i8_res_stats: the dequantised int8 product (exact int32
+  accumulators in the oracle) plus bias and residual, and its statistics.
+- zk_layernorm_q8_res_ln: Add+LayerNorm whose residual is the LayerNorm of
+  given rows from their (mean, rstd), with its int8 quantisation.
 """
 
 import math
@@ -161,3 +165,68 @@ def test_qkv_attn_ln(dev, B, S, heads):
     ok, worst = fp16_tol(y, ref, atol=3e-3, rtol=1.5e-2)
     assert ok, worst
     np.testing.assert_allclose(mr.cpu().numpy(), _ln_stats(x), rtol=1e-5, atol=1e-5)
+
+
+def _i8(shape, seed):
+    return np.random.default_rng(seed).integers(-128, 128, size=shape, dtype=np.int64).astype(np.int8)
+
+
+@pytest.mark.parametrize("M,K,N", [(4096, 3072, 768), (16384, 3072, 768), (300, 2304, 288),
+                                   (100, 64, 96)])
+@pytest.mark.parametrize("ln_res", [False, True])
+def test_gemm_i8_res_stats(dev, M, K, N, ln_res):
+    """zk_gemm_i8_res_stats: the int8 product dequantised (s_x s_w[n]) plus
+    bias and the residual (or its LayerNorm), against the oracle's exact
+    int32 accumulators and fp32 epilogue at the fp16 bar; the segment
+    statistics of the stored output against float64."""
+    qa, qw = _i8((M, K), 70), _i8((N, K), 71)
+    s_x = 0.02
+    s_w = (np.abs(synthetic.normal((N,), tag=72, std=1e-3)) + 1e-4).astype(np.float32)
+    b = synthetic.round_f16(synthetic.normal((N,), tag=73, std=0.1))
+    res = _ln_input(M, N, 74) if ln_res else synthetic.round_f16(synthetic.normal((M, N), tag=74))
+    g, be = _gamma_beta(N, 76)
+    st = _ln_stats(res).astype(np.float32)
+    c = torch.empty((M, N), dtype=torch.float16, device=dev)
+    part = torch.full((M, N // SEG, 2), float("nan"), dtype=torch.float32, device=dev)
+    tqa, tqw = (torch.from_numpy(v).to(dev) for v in (qa, qw))
+    tsw, tst = _t(s_w, dev, torch.float32), _t(st, dev, torch.float32)
+    tb, tr, tg, tbe = (_t(v, dev) for v in (b, res, g, be))
+    print(f"zk_gemm_i8_res_stats M={M} K={K} N={N} ln_res={ln_res}", flush=True)
+    L.call("zk_gemm_i8_res_stats", tqa.data_ptr(), tqw.data_ptr(), c.data_ptr(), M, N, K, K, K, N,
+           s_x, tsw.data_ptr(), tb.data_ptr(), tr.data_ptr(), N,
+           tst.data_ptr() if ln_res else None, tg.data_ptr() if ln_res else None,
+           tbe.data_ptr() if ln_res else None, part.data_ptr(), _stream())
+    torch.cuda.synchronize()
+    y = c.float().cpu().numpy()
+    r = ((res - st[:, :1]) * st[:, 1:] * g + be) if ln_res else res
+    ok, worst = fp16_tol(y, ops.int8_linear(qa, qw, s_x, s_w, b) + r)
+    assert ok, worst
+    np.testing.assert_allclose(part.cpu().numpy(), _seg_stats(y), rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("rows,hidden", [(4096, 768), (333, 768), (7, 100), (64, 1536)])
+def test_layernorm_q8_res_ln(dev, rows, hidden):
+    """zk_layernorm_q8_res_ln: y = LN(x + LN'(r)) with LN' from given
+    per-row (mean, rstd), gamma' and beta', against the oracle's fp32
+    LayerNorm at the fp16 bar; q equal to the oracle's quantisation of the
+    returned y. hidden=100 takes the generic block-per-row kernel."""
+    x = synthetic.round_f16(synthetic.normal((rows, hidden), tag=100))
+    r = _ln_input(rows, hidden, 101)
+    g2, b2 = _gamma_beta(hidden, 104)
+    g1, b1 = _gamma_beta(hidden, 106)
+    st = _ln_stats(r).astype(np.float32)
+    s = 4.0 / 127
+    y = torch.empty((rows, hidden), dtype=torch.float16, device=dev)
+    q = torch.empty((rows, hidden), dtype=torch.int8, device=dev)
+    tx, tr, tg2, tb2, tg1, tb1 = (_t(v, dev) for v in (x, r, g2, b2, g1, b1))
+    tst = _t(st, dev, torch.float32)
+    print(f"zk_layernorm_q8_res_ln rows={rows} hidden={hidden}", flush=True)
+    L.call("zk_layernorm_q8_res_ln", tx.data_ptr(), tr.data_ptr(), tst.data_ptr(), tg2.data_ptr(),
+           tb2.data_ptr(), tg1.data_ptr(), tb1.data_ptr(), y.data_ptr(), q.data_ptr(), rows, hidden,
+           EPS, s, _stream())
+    torch.cuda.synchronize()
+    yn = y.float().cpu().numpy()
+    rl = (r - st[:, :1]) * st[:, 1:] * g2 + b2
+    ok, worst = fp16_tol(yn, ops.add_layernorm(x, rl, g1, b1, EPS))
+    assert ok, worst
+    np.testing.assert_array_equal(q.cpu().numpy(), ops.quantize_int8(yn, s))

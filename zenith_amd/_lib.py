@@ -44,6 +44,8 @@ SIGNATURES: dict[str, list] = {
     "zk_gelu": [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp],
     "zk_layernorm": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp],
     "zk_layernorm_q8": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _f32, _vp],
+    "zk_layernorm_q8_res_ln": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32,
+                               _f32, _vp],
     "zk_layernorm_add": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp],
     "zk_transpose_f16": [_vp, _vp, _i64, _i64, _i64, _i64, _vp],
     "zk_gemm_f16": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
@@ -68,6 +70,8 @@ SIGNATURES: dict[str, list] = {
                    _vp, _vp, _i64, _i32, _i32, _vp],
     "zk_gemm_i8_requant": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _vp,
                            _vp, _i32, _f32, _vp],
+    "zk_gemm_i8_res_stats": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _vp,
+                             _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp],
     "zk_gemm_workspace_size": [_i64, _i64, _i64, _i32],
     "zk_gemm_f16_ws": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
                        _vp, _vp, _i64, _i32, _vp, _i64, _vp],

@@ -847,14 +847,18 @@ static void launch_epi(GemmParams p, int epi, hipStream_t s) {
       break;
     case ZK_EPI_BIAS_RELU: ZK_L(ZK_EPI_BIAS_RELU); break;
     default:
-      // the folded-LayerNorm epilogues: fp16 in and out only; statistics
-      // need wave tiles of whole 32-column segments
+      // the folded-LayerNorm epilogues: fp16 in and out; statistics need
+      // wave tiles of whole kLnSeg-column segments
       if constexpr (std::is_same<OP, F16Op>::value && std::is_same<OutT, f16>::value && !DEQ) {
         if (epi == kEpiLnIn) ZK_L(kEpiLnIn);
         if (epi == kEpiLnInGelu) ZK_L(kEpiLnInGelu);
         if constexpr ((BN / WN) % kLnSeg == 0)
           if (epi == kEpiResStats) ZK_L(kEpiResStats);
       }
+      // the residual + statistics epilogue on the dequantised int8 product
+      if constexpr (std::is_same<OP, I8Op>::value && std::is_same<OutT, f16>::value && DEQ &&
+                    (BN / WN) % kLnSeg == 0)
+        if (epi == kEpiResStats) ZK_L(kEpiResStats);
       break;
   }
 #undef ZK_L
@@ -1230,6 +1234,38 @@ static int check_ln_gemm(const char *who, const void *A, const void *W, const vo
   return check_span(who, lda, ldw, K, 2);
 }
 
+static int check_i8(const char *who, const int8_t *A, const int8_t *W, const void *C, int64_t M,
+                    int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc, int epilogue);
+
+// The residual / statistics operands of zk_gemm_f16_res_stats and
+// zk_gemm_i8_res_stats, checked, then the launch on the configurations whose
+// wave tiles are one statistics segment wide: 256x192 (8 waves) once it
+// fills the CUs, else 128x96 (4 waves).
+template <class OP, bool DEQ>
+static int res_stats_run(const char *who, GemmParams p, const float *res_ln, const void *res_gamma,
+                         const void *res_beta, float *part_out, void *stream) {
+  const int64_t M = p.M, N = p.N;
+  if (!p.bias || !p.res || !part_out)
+    return fail(ZK_ERR_INVALID, "%s: null bias, residual or statistics", who);
+  if (N % kLnSeg) return fail(ZK_ERR_UNSUPPORTED, "%s: N must be a multiple of %d", who, kLnSeg);
+  if (res_ln && (!res_gamma || !res_beta))
+    return fail(ZK_ERR_INVALID, "%s: residual LayerNorm needs gamma and beta", who);
+  if (p.ldr < N) return fail(ZK_ERR_INVALID, "%s: ldr < N", who);
+  if (p.ldr % 8 || !aligned16(p.res))
+    return fail(ZK_ERR_UNSUPPORTED, "%s: residual rows must be 16-byte aligned", who);
+  if (!aligned8(res_ln) || !aligned8(part_out) || !aligned16(res_gamma) || !aligned16(res_beta))
+    return fail(ZK_ERR_UNSUPPORTED,
+                "%s: statistics 8-byte, gamma and beta 16-byte aligned", who);
+  p.res_ln = res_ln;
+  p.res_gamma = res_gamma;
+  p.res_beta = res_beta;
+  p.part_out = part_out;
+  const int64_t t192 = (M + 255) / 256 * (N / 192);
+  launch_mfma<OP, f16, DEQ>(p, kEpiResStats, as_stream(stream),
+                            M >= 1024 && N % 192 == 0 && t192 >= 160 ? 5 : 4);
+  return check_launch(who);
+}
+
 extern "C" int zk_gemm_f16_res_stats(const void *A, const void *W, void *C, int64_t M, int64_t N,
                                      int64_t K, int64_t lda, int64_t ldw, int64_t ldc,
                                      const void *bias, const void *res, int64_t ldr,
@@ -1239,27 +1275,24 @@ extern "C" int zk_gemm_f16_res_stats(const void *A, const void *W, void *C, int6
   int st = check_ln_gemm(who, A, W, C, M, N, K, lda, ldw, ldc);
   if (st) return st;
   if (M == 0 || N == 0) return ZK_OK;
-  if (!bias || !res || !part_out) return fail(ZK_ERR_INVALID, "%s: null bias, residual or statistics", who);
-  if (N % kLnSeg)
-    return fail(ZK_ERR_UNSUPPORTED, "%s: N must be a multiple of %d", who, kLnSeg);
-  if (res_ln && (!res_gamma || !res_beta))
-    return fail(ZK_ERR_INVALID, "%s: residual LayerNorm needs gamma and beta", who);
-  if (ldr < N) return fail(ZK_ERR_INVALID, "%s: ldr < N", who);
-  if (ldr % 8 || !aligned16(res)) return fail(ZK_ERR_UNSUPPORTED, "%s: residual rows must be 16-byte aligned", who);
-  if (!aligned8(res_ln) || !aligned8(part_out) || !aligned16(res_gamma) || !aligned16(res_beta))
-    return fail(ZK_ERR_UNSUPPORTED,
-                "%s: statistics 8-byte, gamma and beta 16-byte aligned", who);
   GemmParams p{A, W, C, (int)M, (int)N, (int)K, lda, ldw, ldc, bias, res, ldr, 1.f, nullptr, 0};
-  p.res_ln = res_ln;
-  p.res_gamma = res_gamma;
-  p.res_beta = res_beta;
-  p.part_out = part_out;
-  // the configurations whose wave tiles are one statistics segment wide:
-  // 256x192 (8 waves) once it fills the CUs, else 128x96 (4 waves)
-  const int64_t t192 = (M + 255) / 256 * (N / 192);
-  launch_mfma<F16Op, f16, false>(p, kEpiResStats, as_stream(stream),
-                                 M >= 1024 && N % 192 == 0 && t192 >= 160 ? 5 : 4);
-  return check_launch(who);
+  return res_stats_run<F16Op, false>(who, p, res_ln, res_gamma, res_beta, part_out, stream);
+}
+
+extern "C" int zk_gemm_i8_res_stats(const int8_t *A, const int8_t *W, void *C, int64_t M,
+                                    int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc,
+                                    float s_x, const float *s_w, const void *bias,
+                                    const void *res, int64_t ldr, const float *res_ln,
+                                    const void *res_gamma, const void *res_beta, float *part_out,
+                                    void *stream) {
+  const char *who = "zk_gemm_i8_res_stats";
+  int st = check_i8(who, A, W, C, M, N, K, lda, ldw, ldc, ZK_EPI_BIAS);
+  if (st || M == 0 || N == 0) return st;
+  if (!s_w || !(s_x > 0.f)) return fail(ZK_ERR_INVALID, "%s: s_w and s_x > 0 are required", who);
+  if (ldc % 8 || !aligned16(C))
+    return fail(ZK_ERR_UNSUPPORTED, "%s: ldc must be a multiple of 8 and C 16-byte aligned", who);
+  GemmParams p{A, W, C, (int)M, (int)N, (int)K, lda, ldw, ldc, bias, res, ldr, s_x, s_w, 0};
+  return res_stats_run<I8Op, true>(who, p, res_ln, res_gamma, res_beta, part_out, stream);
 }
 
 extern "C" int zk_gemm_f16_ln(const void *A, const void *W, void *C, int64_t M, int64_t N,

@@ -18,9 +18,18 @@ template <> struct LnVec<float> { typedef f32x4 type; static constexpr int n = 4
 
 constexpr int kLnWaves = 4;  // wavefronts per 256-thread block
 
-// Residual placement: none, added before the statistics (Add+LayerNorm), or
-// added to the normalised output (LayerNorm+Add).
-enum { kResNone = 0, kResPre = 1, kResPost = 2 };
+// Residual placement: none, added before the statistics (Add+LayerNorm),
+// added to the normalised output (LayerNorm+Add), or added before the
+// statistics as the LayerNorm of the given rows (kResPreLn: r' = (r - mean)
+// rstd g + b with the per-row (mean, rstd) and g, b of that earlier
+// LayerNorm, computed on the fly in fp32).
+enum { kResNone = 0, kResPre = 1, kResPost = 2, kResPreLn = 3 };
+
+// The earlier LayerNorm of the residual rows (kResPreLn).
+template <typename T> struct ResLn {
+  const float2 *ms;  // [rows] (mean, rstd)
+  const T *g, *b;    // [hidden]
+};
 
 // LPR lanes per row (64 / LPR rows per wavefront): a 768-wide fp16 row is 96
 // 16-byte vectors, so two rows per wavefront give every lane exactly three.
@@ -30,7 +39,8 @@ template <typename T, int MAXV, int RES, int LPR, bool Q8>
 __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
     const T *__restrict__ x, const T *__restrict__ res,
     const T *__restrict__ gamma, const T *__restrict__ beta, T *__restrict__ y,
-    int8_t *__restrict__ q, float qs, int64_t rows, int hidden, float eps) {
+    int8_t *__restrict__ q, float qs, int64_t rows, int hidden, float eps, ResLn<T> rl) {
+  constexpr bool PRE = RES == kResPre || RES == kResPreLn;
   typedef typename LnVec<T>::type V;
   constexpr int W = LnVec<T>::n;
   constexpr int RPW = kWave / LPR;  // rows per wavefront
@@ -43,6 +53,8 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
   const int nvec = hidden / W;
   const V *xr = reinterpret_cast<const V *>(x + (live ? row : 0) * hidden);
   const V *rr = reinterpret_cast<const V *>(res + (RES != kResNone && live ? row * hidden : 0));
+  float2 rms = make_float2(0.f, 1.f);
+  if constexpr (RES == kResPreLn) rms = rl.ms[live ? row : 0];
 
   float v[MAXV][W];
   float sum = 0.f;
@@ -51,12 +63,18 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
     const int idx = sub + k * LPR;
     if (live && idx < nvec) {
       V a = xr[idx];
-      V r;
-      if (RES == kResPre) r = rr[idx];
+      V r, rg, rb;
+      if (PRE) r = rr[idx];
+      if (RES == kResPreLn) {
+        rg = reinterpret_cast<const V *>(rl.g)[idx];
+        rb = reinterpret_cast<const V *>(rl.b)[idx];
+      }
 #pragma unroll
       for (int j = 0; j < W; ++j) {
         float f = (float)a[j];
         if (RES == kResPre) f += (float)r[j];
+        if (RES == kResPreLn)
+          f += fmaf(((float)r[j] - rms.x) * rms.y, (float)rg[j], (float)rb[j]);
         v[k][j] = f;
         sum += f;
       }
@@ -122,12 +140,19 @@ template <typename T, int RES, bool Q8>
 __global__ __launch_bounds__(256) void ln_block_kernel(
     const T *__restrict__ x, const T *__restrict__ res,
     const T *__restrict__ gamma, const T *__restrict__ beta, T *__restrict__ y,
-    int8_t *__restrict__ q, float qs, int64_t hidden, float eps) {
+    int8_t *__restrict__ q, float qs, int64_t hidden, float eps, ResLn<T> rl) {
   __shared__ float part[256 / kWave];
   const int64_t row = blockIdx.x;
   const T *xr = x + row * hidden;
   const T *rr = RES != kResNone ? res + row * hidden : nullptr;
-  constexpr bool PRE = RES == kResPre;
+  constexpr bool PRE = RES == kResPre || RES == kResPreLn;
+  const float2 rms = RES == kResPreLn ? rl.ms[row] : make_float2(0.f, 1.f);
+  // the residual's value at column i (kResPreLn: its LayerNorm)
+  auto rv = [&](int64_t i) {
+    if constexpr (RES == kResPreLn)
+      return fmaf(((float)rr[i] - rms.x) * rms.y, (float)rl.g[i], (float)rl.b[i]);
+    return (float)rr[i];
+  };
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid >> 6;
   constexpr int NW = 256 / kWave;
 
@@ -144,16 +169,16 @@ __global__ __launch_bounds__(256) void ln_block_kernel(
 
   float s = 0.f;
   for (int64_t i = tid; i < hidden; i += 256)
-    s += (float)xr[i] + (PRE ? (float)rr[i] : 0.f);
+    s += (float)xr[i] + (PRE ? rv(i) : 0.f);
   const float mean = block_sum(s) / (float)hidden;
   float sq = 0.f;
   for (int64_t i = tid; i < hidden; i += 256) {
-    const float d = (float)xr[i] + (PRE ? (float)rr[i] : 0.f) - mean;
+    const float d = (float)xr[i] + (PRE ? rv(i) : 0.f) - mean;
     sq += d * d;
   }
   const float rstd = 1.0f / sqrtf(block_sum(sq) / (float)hidden + eps);
   for (int64_t i = tid; i < hidden; i += 256) {
-    const float f = (float)xr[i] + (PRE ? (float)rr[i] : 0.f);
+    const float f = (float)xr[i] + (PRE ? rv(i) : 0.f);
     float yv = (f - mean) * rstd * (float)gamma[i] + (float)beta[i];
     if (RES == kResPost) yv += (float)rr[i];
     const T o = (T)yv;
@@ -165,41 +190,46 @@ __global__ __launch_bounds__(256) void ln_block_kernel(
 template <typename T, int MAXV, int LPR, bool Q8>
 static void ln_wave_launch(const T *x, const T *r, const T *g, const T *b, T *y, int8_t *q,
                            float qs, int64_t rows, int hidden, float eps, bool post,
-                           hipStream_t s) {
+                           ResLn<T> rl, hipStream_t s) {
   constexpr int rows_per_block = kLnWaves * (kWave / LPR);
   const unsigned grid = (unsigned)((rows + rows_per_block - 1) / rows_per_block);
+#define ZK_LNW(RES, QQ) \
+  ln_wave_kernel<T, MAXV, RES, LPR, QQ><<<grid, kLnWaves * kWave, 0, s>>>(x, r, g, b, y, q, qs, \
+                                                                         rows, hidden, eps, rl)
   if (r && post) {
-    if constexpr (!Q8)
-      ln_wave_kernel<T, MAXV, kResPost, LPR, false><<<grid, kLnWaves * kWave, 0, s>>>(
-          x, r, g, b, y, q, qs, rows, hidden, eps);
+    if constexpr (!Q8) ZK_LNW(kResPost, false);
+  } else if (r && rl.ms) {
+    if constexpr (Q8) ZK_LNW(kResPreLn, true);
   } else if (r) {
-    ln_wave_kernel<T, MAXV, kResPre, LPR, Q8><<<grid, kLnWaves * kWave, 0, s>>>(
-        x, r, g, b, y, q, qs, rows, hidden, eps);
+    ZK_LNW(kResPre, Q8);
   } else {
-    ln_wave_kernel<T, MAXV, kResNone, LPR, Q8><<<grid, kLnWaves * kWave, 0, s>>>(
-        x, r, g, b, y, q, qs, rows, hidden, eps);
+    ZK_LNW(kResNone, Q8);
   }
+#undef ZK_LNW
 }
 
 // post: the residual is added after normalisation (LN(x) + r) instead of
-// before it (LN(x + r)); never combined with the int8 output.
+// before it (LN(x + r)); never combined with the int8 output. rl.ms set: the
+// residual is the LayerNorm of r (int8 output only).
 template <typename T, bool Q8>
 static int ln_impl(const void *xv, const void *rv, const void *gv,
                    const void *bv, void *yv, int8_t *q, float qs, int64_t rows,
-                   int64_t hidden, float eps, hipStream_t s, bool post = false) {
+                   int64_t hidden, float eps, hipStream_t s, bool post = false,
+                   ResLn<T> rl = ResLn<T>{nullptr, nullptr, nullptr}) {
   const T *x = (const T *)xv, *r = (const T *)rv, *g = (const T *)gv,
           *b = (const T *)bv;
   T *y = (T *)yv;
   constexpr int W = LnVec<T>::n;
   const bool vec_ok = hidden % W == 0 && aligned16(x) && aligned16(y) &&
                       aligned16(g) && aligned16(b) && (!r || aligned16(r)) &&
-                      (!Q8 || aligned8(q));
+                      (!Q8 || aligned8(q)) && (!rl.ms || (aligned16(rl.g) && aligned16(rl.b)));
   const int64_t nvec = hidden / W;
   if (vec_ok && nvec <= 16 * kWave && (rows + kLnWaves - 1) / kLnWaves <= 0x7fffffff) {
     const int h = (int)hidden;
     // 32 lanes per row while a row fits in 4 vectors per lane (H <= 1024 in
     // fp16), else a whole wavefront per row.
-#define ZK_LN(MV, LPR) ln_wave_launch<T, MV, LPR, Q8>(x, r, g, b, y, q, qs, rows, h, eps, post, s)
+#define ZK_LN(MV, LPR) \
+  ln_wave_launch<T, MV, LPR, Q8>(x, r, g, b, y, q, qs, rows, h, eps, post, rl, s)
     if (nvec <= 32) ZK_LN(1, 32);
     else if (nvec <= 64) ZK_LN(2, 32);
     else if (nvec <= 96) ZK_LN(3, 32);
@@ -211,15 +241,18 @@ static int ln_impl(const void *xv, const void *rv, const void *gv,
   } else {
     if (rows > 0x7fffffff)
       return fail(ZK_ERR_UNSUPPORTED, "zk_layernorm: too many rows for the generic path");
+#define ZK_LNB(RES, QQ) \
+  ln_block_kernel<T, RES, QQ><<<(unsigned)rows, 256, 0, s>>>(x, r, g, b, y, q, qs, hidden, eps, rl)
     if (r && post) {
-      if constexpr (!Q8)
-        ln_block_kernel<T, kResPost, false><<<(unsigned)rows, 256, 0, s>>>(x, r, g, b, y, q, qs,
-                                                                          hidden, eps);
+      if constexpr (!Q8) ZK_LNB(kResPost, false);
+    } else if (r && rl.ms) {
+      if constexpr (Q8) ZK_LNB(kResPreLn, true);
     } else if (r) {
-      ln_block_kernel<T, kResPre, Q8><<<(unsigned)rows, 256, 0, s>>>(x, r, g, b, y, q, qs, hidden, eps);
+      ZK_LNB(kResPre, Q8);
     } else {
-      ln_block_kernel<T, kResNone, Q8><<<(unsigned)rows, 256, 0, s>>>(x, r, g, b, y, q, qs, hidden, eps);
+      ZK_LNB(kResNone, Q8);
     }
+#undef ZK_LNB
   }
   return check_launch("zk_layernorm");
 }
@@ -261,6 +294,24 @@ extern "C" int zk_layernorm_q8(const void *x, const void *residual, const void *
   if (!(q_scale > 0.f)) return fail(ZK_ERR_INVALID, "zk_layernorm_q8: q_scale must be > 0");
   return ln_impl<f16, true>(x, residual, gamma, beta, y, q, q_scale, rows, hidden, eps,
                             as_stream(stream));
+}
+
+extern "C" int zk_layernorm_q8_res_ln(const void *x, const void *residual, const float *res_ln,
+                                      const void *res_gamma, const void *res_beta,
+                                      const void *gamma, const void *beta, void *y, int8_t *q,
+                                      int64_t rows, int64_t hidden, float eps, float q_scale,
+                                      void *stream) {
+  const char *who = "zk_layernorm_q8_res_ln";
+  int st = ln_check(who, x, gamma, beta, y, rows, hidden, eps);
+  if (st || rows == 0) return st;
+  if (!q || !residual || !res_ln || !res_gamma || !res_beta)
+    return fail(ZK_ERR_INVALID, "%s: null pointer", who);
+  if (!(q_scale > 0.f)) return fail(ZK_ERR_INVALID, "%s: q_scale must be > 0", who);
+  if (!aligned8(res_ln)) return fail(ZK_ERR_UNSUPPORTED, "%s: res_ln must be 8-byte aligned", who);
+  return ln_impl<f16, true>(x, residual, gamma, beta, y, q, q_scale, rows, hidden, eps,
+                            as_stream(stream), false,
+                            ResLn<f16>{(const float2 *)res_ln, (const f16 *)res_gamma,
+                                       (const f16 *)res_beta});
 }
 
 extern "C" int zk_layernorm_add(const void *x, const void *residual, const void *gamma,

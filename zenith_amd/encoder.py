@@ -16,12 +16,15 @@ One post-LN layer is seven launches, in the reference encoder's order
   6. FFN-down GEMM + bias       u . Wo2^T                     -> t[M,H]
   7. Add+LayerNorm              LN(t + h1)                    -> out[M,H]
 
-The INT8-FFN variant keeps seven launches: step 4 also writes the int8
-quantisation of h1, step 5 is an int8 GEMM whose epilogue dequantises, adds
-the bias, applies GELU and re-quantises (int8 out), and step 6 is an int8
-GEMM with a dequant + bias epilogue. The int8 values equal those of the
-unfused sequence (quantise the fp16 tensor), since both quantise the same
-fp16-rounded value.
+In the INT8-FFN variant step 4 also writes the int8 quantisation of h1,
+step 5 is an int8 GEMM whose epilogue dequantises, adds the bias, applies
+GELU and re-quantises (int8 out), and step 6 is an int8 GEMM with a dequant
++ bias epilogue. The int8 values equal those of the unfused sequence
+(quantise the fp16 tensor), since both quantise the same fp16-rounded value.
+
+With fold_layernorm (the default) the LayerNorms are folded into the GEMMs
+that consume them (see _run_folded): four launches per fp16 layer, five
+with the INT8 FFN.
 
 All activations live in buffers allocated once per (batch, seq); the whole
 forward can be captured into a HIP graph (torch.cuda.CUDAGraph) and replayed,
@@ -144,6 +147,16 @@ class BertEncoder:
         launch (zk_qkv_attn_f16: S of 64 or 128, head_dim 64)."""
         return self.fuse_qkv_attention and S in (64, 128) and self.head_dim == 64
 
+    def folded(self, S: int) -> bool:
+        """Whether sequences of S tokens run with the LayerNorms folded into
+        the GEMMs. With the INT8 FFN only where the QKV projection and
+        attention are one launch: at b32 s128 folding took the INT8-FFN
+        encoder from 1.064 to 1.034 ms per step, at s512 from 3.558 to 3.608
+        (the residual and statistics epilogue of the 256x192-tile int8
+        FFN-down and the LayerNorm-folded 256x256 QKV GEMM cost more than the
+        Add+LayerNorm launch they replace)."""
+        return self.fold_ln and (self.int8 is None or self.fused_attention(S))
+
     # ------------------------------------------------------------ INT8 FFN --
     def enable_int8_ffn(self, s_x: list[float], s_h: list[float], layers_fp32: list[dict] | None = None):
         """Switch the FFN to int8 with per-layer activation scales s_x (FFN-up
@@ -252,7 +265,7 @@ class BertEncoder:
         bf = self._bufs
         stream = torch.cuda.current_stream(self.device).cuda_stream
         stop = len(self.layers) if stop is None else stop
-        if self.fold_ln and self.int8 is None:
+        if self.folded(S):
             return self._run_folded(x2, lens, B, S, out, start, stop, stream)
         cur = x2
         for i in range(start, stop):
@@ -268,7 +281,10 @@ class BertEncoder:
         layer's QKV projection applies LN2 through its folded weights and
         its out-projection adds LN2(h2) as the residual on the fly; LN1 goes
         the same way into FFN-up and FFN-down. One LayerNorm kernel at the
-        end materialises the last output."""
+        end materialises the last output. With the INT8 FFN, LN1 is
+        materialised together with its int8 copy (its LN2 residual applied
+        on the fly) and the int8 FFN-down writes h2 with its statistics:
+        five launches per layer."""
         bf = self._bufs
         H, D, nh, I = self.hidden, self.head_dim, self.heads, self.ffn
         M, eps = B * S, self.eps
@@ -301,20 +317,45 @@ class BertEncoder:
                            w["s_qkv"].data_ptr(), w["c_qkv"].data_ptr(), mr2.data_ptr(),
                            L.ZK_EPI_BIAS, stream)
                 self._attention(qkv, ctx, lens, B, S, stream)
-            # 3. out-projection + residual (the input, or LN2(input)) -> h, stats
-            L.call("zk_gemm_f16_res_stats", ctx.data_ptr(), w["Wo"].data_ptr(), h.data_ptr(),
-                   M, H, H, H, H, H, w["bo"].data_ptr(), cur.data_ptr(), H,
-                   None if first else mr2.data_ptr(),
-                   None if first else prev["ln2_g"].data_ptr(),
-                   None if first else prev["ln2_b"].data_ptr(), p1.data_ptr(), stream)
-            # 4. FFN-up on LN1(h) + GELU
-            L.call("zk_gemm_f16_ln", h.data_ptr(), w["Wi_f"].data_ptr(), u.data_ptr(), M, I, H, H,
-                   H, I, p1.data_ptr(), self.eps, w["s_i"].data_ptr(), w["c_i"].data_ptr(),
-                   mr1.data_ptr(), L.ZK_EPI_BIAS_GELU_ERF, stream)
-            # 5. FFN-down + LN1(h) -> h2, stats
-            L.call("zk_gemm_f16_res_stats", u.data_ptr(), w["Wo2"].data_ptr(), h2.data_ptr(),
-                   M, H, I, I, I, H, w["bo2"].data_ptr(), h.data_ptr(), H, mr1.data_ptr(),
-                   w["ln1_g"].data_ptr(), w["ln1_b"].data_ptr(), p2.data_ptr(), stream)
+            if self.int8 is None:
+                # 3. out-projection + residual (the input, or LN2(input)) -> h, stats
+                L.call("zk_gemm_f16_res_stats", ctx.data_ptr(), w["Wo"].data_ptr(), h.data_ptr(),
+                       M, H, H, H, H, H, w["bo"].data_ptr(), cur.data_ptr(), H,
+                       None if first else mr2.data_ptr(),
+                       None if first else prev["ln2_g"].data_ptr(),
+                       None if first else prev["ln2_b"].data_ptr(), p1.data_ptr(), stream)
+                # 4. FFN-up on LN1(h) + GELU
+                L.call("zk_gemm_f16_ln", h.data_ptr(), w["Wi_f"].data_ptr(), u.data_ptr(), M, I, H,
+                       H, H, I, p1.data_ptr(), self.eps, w["s_i"].data_ptr(), w["c_i"].data_ptr(),
+                       mr1.data_ptr(), L.ZK_EPI_BIAS_GELU_ERF, stream)
+                # 5. FFN-down + LN1(h) -> h2, stats
+                L.call("zk_gemm_f16_res_stats", u.data_ptr(), w["Wo2"].data_ptr(), h2.data_ptr(),
+                       M, H, I, I, I, H, w["bo2"].data_ptr(), h.data_ptr(), H, mr1.data_ptr(),
+                       w["ln1_g"].data_ptr(), w["ln1_b"].data_ptr(), p2.data_ptr(), stream)
+            else:
+                # INT8 FFN (five launches): LN1 is materialised, with its int8
+                # copy for FFN-up; LN2 stays folded as in the fp16 layer.
+                q, qh, qu, t = self.int8[i], bf["q_h"], bf["q_u"], bf["t"]
+                # 3. out-projection + bias -> t
+                self._gemm(ctx, w["Wo"], w["bo"], t, L.ZK_EPI_BIAS, stream=stream)
+                # 4. h = LN1(t + the input, or + LN2(input) on the fly), and q(h)
+                if first:
+                    L.call("zk_layernorm_q8", t.data_ptr(), cur.data_ptr(), w["ln1_g"].data_ptr(),
+                           w["ln1_b"].data_ptr(), h.data_ptr(), qh.data_ptr(), M, H, self.eps,
+                           q["s_x"], stream)
+                else:
+                    L.call("zk_layernorm_q8_res_ln", t.data_ptr(), cur.data_ptr(), mr2.data_ptr(),
+                           prev["ln2_g"].data_ptr(), prev["ln2_b"].data_ptr(),
+                           w["ln1_g"].data_ptr(), w["ln1_b"].data_ptr(), h.data_ptr(),
+                           qh.data_ptr(), M, H, self.eps, q["s_x"], stream)
+                # 5. FFN-up int8 + bias + GELU, re-quantised
+                L.call("zk_gemm_i8_requant", qh.data_ptr(), q["Wi_q"].data_ptr(), qu.data_ptr(), M,
+                       I, H, H, H, I, q["s_x"], q["s_wi"].data_ptr(), w["bi"].data_ptr(),
+                       self.gelu_epi, q["s_h"], stream)
+                # 6. FFN-down int8 + bias + h -> h2, stats
+                L.call("zk_gemm_i8_res_stats", qu.data_ptr(), q["Wo2_q"].data_ptr(), h2.data_ptr(),
+                       M, H, I, I, I, H, q["s_h"], q["s_wo2"].data_ptr(), w["bo2"].data_ptr(),
+                       h.data_ptr(), H, None, None, None, p2.data_ptr(), stream)
             cur, cur_parts = h2, p2
         w = self.layers[stop - 1]
         L.call("zk_layernorm", cur.data_ptr(), None, w["ln2_g"].data_ptr(), w["ln2_b"].data_ptr(),
