@@ -116,22 +116,31 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 
 // Branch-free forms for GEMM epilogues (fp16 outputs), with the constant
 // factors folded so that each costs as few VALU instructions as possible.
-// erf by Abramowitz & Stegun 7.1.26: for z >= 0,
-//   erf(z) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-z^2),
-//   t = 1 / (1 + p z), |error| <= 1.5e-7.
-// With z = |x| / sqrt(2) and h = (1 - erf(z)) / 2 (the halves folded into
-// the a_k): GELU(x) = x (1 - h) for x >= 0 and x h for x < 0, which are both
-// max(x, 0) - |x| h (a max and one fma instead of a select).
+// erf by Abramowitz & Stegun 7.1.28: for z >= 0,
+//   erf(z) = 1 - (1 + a1 z + a2 z^2 + ... + a6 z^6)^-16, |error| <= 3e-7,
+// a polynomial, four squarings and one reciprocal (7.1.26 needs a
+// reciprocal and an exponential, both quarter-rate transcendentals).
+// With z = |x| / sqrt(2) (folded into the a_k) and r = 1 - erf(z):
+// GELU(x) = x (1 - r / 2) for x >= 0 and x r / 2 for x < 0, which are both
+// max(x, 0) - |x| r / 2 (a max and one fma instead of a select). Measured
+// against the exact GELU on [-8, 8] in fp32: at most 7.1e-7 absolute.
+// For |x| beyond about 19 the 16th power overflows to inf and r is 0:
+// GELU(x) = max(x, 0), which it equals there to far below fp32 resolution.
 __device__ __forceinline__ float gelu_erf_fast(float x) {
-  const float t = __builtin_amdgcn_rcpf(fmaf(fabsf(x), 0.3275911f * 0.70710678118654752f, 1.0f));
-  float q = 0.5f * 1.061405429f;
-  q = fmaf(q, t, 0.5f * -1.453152027f);
-  q = fmaf(q, t, 0.5f * 1.421413741f);
-  q = fmaf(q, t, 0.5f * -0.284496736f);
-  q = fmaf(q, t, 0.5f * 0.254829592f);
-  // exp(-z^2) = exp2(-x^2 log2(e) / 2)
-  const float h = q * t * __builtin_amdgcn_exp2f(x * x * (-0.5f * 1.4426950408889634f));
-  return fmaf(-fabsf(x), h, fmaxf(x, 0.f));
+  constexpr float s = 0.70710678118654752f;  // 1 / sqrt(2)
+  const float ax = fabsf(x);
+  float p = 0.0000430638f * (s * s * s * s * s * s);
+  p = fmaf(p, ax, 0.0002765672f * (s * s * s * s * s));
+  p = fmaf(p, ax, 0.0001520143f * (s * s * s * s));
+  p = fmaf(p, ax, 0.0092705272f * (s * s * s));
+  p = fmaf(p, ax, 0.0422820123f * (s * s));
+  p = fmaf(p, ax, 0.0705230784f * s);
+  p = fmaf(p, ax, 1.0f);
+  p *= p;
+  p *= p;
+  p *= p;
+  p *= p;
+  return fmaf(ax * __builtin_amdgcn_rcpf(p), -0.5f, fmaxf(x, 0.f));
 }
 // tanh(y) = 1 - 2 / (1 + exp(2y)) (exact identity), so
 // 0.5 x (1 + tanh(y)) = x - x / (1 + exp(2y)), y = sqrt(2/pi) (x + 0.044715 x^3).
