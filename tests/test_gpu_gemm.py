@@ -262,7 +262,7 @@ def test_linear_f32_c_abi(dev, M, K, N, epi):
     kernel (K % 4 == 0), the SIMT kernel with its separate epilogue pass
     (K = 70) and split-K with the epilogue in the ordered reduction (M = 16),
     each epilogue against the float64 product; rtol 1e-4 (fp32 products and
-    accumulation; erf-GELU within 7.1e-7 absolute)."""
+    accumulation; erf-GELU within 7.2e-7 absolute)."""
     from zenith_amd import _lib as L
     from zenith_amd.zenith_cuda import _ws_args, gemm_workspace
 

@@ -116,31 +116,28 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 
 // Branch-free forms for GEMM epilogues (fp16 outputs), with the constant
 // factors folded so that each costs as few VALU instructions as possible.
-// erf by Abramowitz & Stegun 7.1.28: for z >= 0,
-//   erf(z) = 1 - (1 + a1 z + a2 z^2 + ... + a6 z^6)^-16, |error| <= 3e-7,
-// a polynomial, four squarings and one reciprocal (7.1.26 needs a
-// reciprocal and an exponential, both quarter-rate transcendentals).
-// With z = |x| / sqrt(2) (folded into the a_k) and r = 1 - erf(z):
-// GELU(x) = x (1 - r / 2) for x >= 0 and x r / 2 for x < 0, which are both
-// max(x, 0) - |x| r / 2 (a max and one fma instead of a select). Measured
-// against the exact GELU on [-8, 8] in fp32: at most 7.1e-7 absolute.
-// For |x| beyond about 19 the 16th power overflows to inf and r is 0:
-// GELU(x) = max(x, 0), which it equals there to far below fp32 resolution.
+// erf-GELU: GELU(x) = x Phi(x) = max(x, 0) - |x| Phi(-|x|) for either sign
+// (Phi the standard normal CDF), and Phi(-a) = 2^p(a) with p a degree-5
+// polynomial, p(0) = -1 exactly (Phi(0) = 1/2), fitted to log2 Phi(-a) on
+// [0, 8] by weighted minimax: a linear program over 4000 Chebyshev points
+// with weight a Phi(-a) ln 2, the absolute error of the product per unit
+// error in p (fit_gelu_poly.py beside this file prints the coefficients).
+// The leading coefficient is negative and p falls monotonically beyond the
+// fitted range (p < -52 for every a > 8), so 2^p underflows to 0 and
+// GELU(x) = max(x, 0) there without a clamp. Evaluated in fp32 (Horner with
+// fma, v_exp_f32): at most 7.2e-7 absolute against the exact GELU on
+// [-12, 12] (the fp32 rounding of the result alone is up to 2.4e-7), and
+// 6e-6 relative for 0 < |x| <= 1. Eight instructions, one of them
+// transcendental (quarter rate, so it costs four).
 __device__ __forceinline__ float gelu_erf_fast(float x) {
-  constexpr float s = 0.70710678118654752f;  // 1 / sqrt(2)
-  const float ax = fabsf(x);
-  float p = 0.0000430638f * (s * s * s * s * s * s);
-  p = fmaf(p, ax, 0.0002765672f * (s * s * s * s * s));
-  p = fmaf(p, ax, 0.0001520143f * (s * s * s * s));
-  p = fmaf(p, ax, 0.0092705272f * (s * s * s));
-  p = fmaf(p, ax, 0.0422820123f * (s * s));
-  p = fmaf(p, ax, 0.0705230784f * s);
-  p = fmaf(p, ax, 1.0f);
-  p *= p;
-  p *= p;
-  p *= p;
-  p *= p;
-  return fmaf(ax * __builtin_amdgcn_rcpf(p), -0.5f, fmaxf(x, 0.f));
+  const float a = fabsf(x);
+  float p = -4.891129793e-04f;
+  p = fmaf(p, a, 7.206471637e-03f);
+  p = fmaf(p, a, -5.216677114e-02f);
+  p = fmaf(p, a, -4.595749378e-01f);
+  p = fmaf(p, a, -1.151007652e+00f);
+  p = fmaf(p, a, -1.0f);
+  return fmaf(-a, __builtin_amdgcn_exp2f(p), fmaxf(x, 0.f));
 }
 // tanh(y) = 1 - 2 / (1 + exp(2y)) (exact identity), so
 // 0.5 x (1 + tanh(y)) = x - x / (1 + exp(2y)), y = sqrt(2/pi) (x + 0.044715 x^3).

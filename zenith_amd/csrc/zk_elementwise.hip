@@ -82,7 +82,7 @@ static int unary_entry(const void *x, void *y, int64_t n, int dtype, void *strea
 
 // ------------------------------------------------------------------ GELU --
 // fp16 outputs use the branch-free forms of the GEMM epilogues (GELU within
-// 7.1e-7 absolute, far below fp16's 4.9e-4 relative step), so the kernel stays
+// 7.2e-7 absolute, far below fp16's 4.9e-4 relative step), so the kernel stays
 // bound by HBM rather than by libm's erff / tanhf; fp32 keeps the exact forms.
 template <typename T, int MODE>
 __device__ __forceinline__ float gelu(float v) {
