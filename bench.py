@@ -168,14 +168,73 @@ def kernel_cases(torch, dev):
             c = torch.empty((M, N), dtype=torch.int8 if requant else f16, device=dev)
             keep = (a, w, sw, b, c)
             if requant:
+                # an absmax/127 output scale, as calibration gives the encoder.
+                # With a scale of 1/20, about one fp16 GELU output in 600 lands
+                # on (or within 6e-5 of) a rounding tie, and 60% of the
+                # wavefront-wide store vectors take the quantiser's exact-
+                # division path; with 6/127 it is one value in 9000 and 5% of
+                # the vectors, as with calibrated scales.
                 args = (a.data_ptr(), w.data_ptr(), c.data_ptr(), M, N, K, K, K, N, 0.01,
-                        sw.data_ptr(), b.data_ptr(), epi, 0.05)
+                        sw.data_ptr(), b.data_ptr(), epi, 6.0 / 127)
                 return (lambda i: _rc(L, lib.zk_gemm_i8_requant(*args, s())) and keep), \
                     2.0 * M * N * K, "TOP/s", "int8", "mfma", f"M={M} K={K} N={N} int8 out"
             args = (a.data_ptr(), w.data_ptr(), c.data_ptr(), M, N, K, K, K, N, 0.01,
                     sw.data_ptr(), b.data_ptr(), None, 0, epi, L.ZK_F16)
             return (lambda i: _rc(L, lib.zk_gemm_i8(*args, s())) and keep), 2.0 * M * N * K, \
                 "TOP/s", "int8", "mfma", f"M={M} K={K} N={N}"
+        return setup
+
+    def res_stats_i8(M, K, N):
+        """The INT8-FFN encoder's FFN-down with LayerNorm 2 folded: int8
+        product, dequantisation, bias, the residual LayerNorm-ed on the fly,
+        fp16 output and per-row statistics."""
+        def setup():
+            a = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev)
+            w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev)
+            sw = torch.full((N,), 1e-3, dtype=torch.float32, device=dev)
+            b = torch.zeros(N, dtype=f16, device=dev)
+            r = torch.from_numpy(synthetic.normal((M, N), tag=3)).to(dev, f16)
+            c = torch.empty((M, N), dtype=f16, device=dev)
+            ms = torch.zeros((M, 2), dtype=torch.float32, device=dev)
+            ms[:, 1] = 1.0
+            g = torch.ones(N, dtype=f16, device=dev)
+            be = torch.zeros(N, dtype=f16, device=dev)
+            part = torch.empty((M, N // 96, 2), dtype=torch.float32, device=dev)
+            keep = (a, w, sw, b, r, c, ms, g, be, part)
+            args = (a.data_ptr(), w.data_ptr(), c.data_ptr(), M, N, K, K, K, N, 0.01,
+                    sw.data_ptr(), b.data_ptr(), r.data_ptr(), N, ms.data_ptr(), g.data_ptr(),
+                    be.data_ptr(), part.data_ptr())
+            return (lambda i: _rc(L, lib.zk_gemm_i8_res_stats(*args, s())) and keep), \
+                2.0 * M * N * K, "TOP/s", "int8", "mfma", \
+                f"M={M} K={K} N={N} + residual LayerNorm + row statistics"
+        return setup
+
+    def add_ln_q8_res_ln(M=4096):
+        """The INT8-FFN encoder's Add+LayerNorm 1: x + LN2(residual) from the
+        residual's row statistics, LayerNorm, fp16 and int8 outputs."""
+        def setup():
+            H = 768
+            per = 7 * M * H + 8 * M  # x, residual, y (fp16), q (int8), statistics
+            n = max(2, (512 << 20) // per + 1)  # rotate past the 256 MB MALL
+            xs = [torch.randn(M, H, device=dev, dtype=f16) for _ in range(n)]
+            rs = [torch.randn(M, H, device=dev, dtype=f16) for _ in range(n)]
+            mss = [torch.stack([torch.zeros(M, device=dev), torch.ones(M, device=dev)], 1)
+                   for _ in range(n)]
+            ys = [torch.empty(M, H, device=dev, dtype=f16) for _ in range(n)]
+            qs = [torch.empty(M, H, device=dev, dtype=torch.int8) for _ in range(n)]
+            g = torch.ones(H, device=dev, dtype=f16)
+            b = torch.zeros(H, device=dev, dtype=f16)
+            keep = (xs, rs, mss, ys, qs, g, b)
+
+            def launch(i):
+                j = i % n
+                _rc(L, lib.zk_layernorm_q8_res_ln(
+                    xs[j].data_ptr(), rs[j].data_ptr(), mss[j].data_ptr(), g.data_ptr(),
+                    b.data_ptr(), g.data_ptr(), b.data_ptr(), ys[j].data_ptr(), qs[j].data_ptr(),
+                    M, H, 1e-12, 0.05, s()))
+                return keep
+            return launch, float(per), "GB/s", "hbm", "hbm", \
+                f"[{M},{H}] fp16 + int8 out, residual LayerNorm-ed, {n} rotating buffer sets"
         return setup
 
     def attn(S):
@@ -372,6 +431,9 @@ def kernel_cases(torch, dev):
         "attn_s512": attn(512),
         "int8_ffn_up": gemm_i8(4096, 768, 3072, L.ZK_EPI_BIAS_GELU_ERF, requant=True),
         "int8_ffn_down": gemm_i8(4096, 3072, 768, E),
+        # the INT8-FFN layer's own launches at b32 s128 (LayerNorm 2 folded)
+        "int8_ffn_down_res_stats": res_stats_i8(4096, 3072, 768),
+        "add_layernorm_q8_res_ln": add_ln_q8_res_ln(),
         "add_layernorm": add_ln(),
         "bias_gelu": bias_gelu(),
         # config 5 at seq 512 (M = 32 x 512): the sizes where the HBM target
