@@ -215,15 +215,17 @@ def test_flash_attention_uniform_keys(dev):
         np.testing.assert_allclose(o[b], np.broadcast_to(mean, o[b].shape), atol=2e-3, rtol=1e-2)
 
 
-def test_flash_attention_strided_qkv(dev):
+@pytest.mark.parametrize("S,lens", [(128, [128, 70, 64]), (512, [512, 300, 65])])
+def test_flash_attention_strided_qkv(dev, S, lens):
     """Q/K/V read by stride out of a packed [B*S, 3H] projection, O written
-    into [B*S, H]: the layout the encoder uses (no transposes)."""
+    into [B*S, H]: the layout the encoder uses (no transposes). At S = 512
+    the K/V rows are 3H apart in the DMA ring kernel's buffer reads."""
     from zenith_amd import _lib as L
 
-    B, S, nh, D = 3, 128, 12, 64
+    B, nh, D = 3, 12, 64
     H = nh * D
     qkv = synthetic.round_f16(synthetic.normal((B * S, 3 * H), tag=40))
-    lens = np.array([128, 70, 64], np.int32)
+    lens = np.array(lens, np.int32)
     tq = torch.from_numpy(qkv).to(dev, torch.float16)
     out = torch.empty((B * S, H), dtype=torch.float16, device=dev)
     base, es = tq.data_ptr(), 2
@@ -263,6 +265,21 @@ def test_flash_attention_long_queries_ragged_keys(dev, Sk, lens):
     rows past Sk must read as zeros; lengths 0, 1, a tile boundary, Sk."""
     q, _, _ = _qkv(4, 3, 128, 128, 64, tag=80)
     _, k, v = _qkv(4, 3, Sk, Sk, 64, tag=85)
+    lens = np.array(lens, np.int32)
+    o = _run(dev, q, k, v, lens, torch.float16)
+    assert np.all(o[lens == 0] == 0)
+    ok, worst = fp16_tol(o, ops.attention(q, k, v, lens))
+    assert ok, worst
+
+
+@pytest.mark.parametrize("Sk,lens", [(450, [450, 0, 1, 64]), (200, [129, 200, 63, 2])])
+def test_flash_attention_ring_ragged_keys(dev, Sk, lens):
+    """From 384 queries (D = 64, lengths only) K and V reach LDS by DMA into a
+    ring of tile stages: Sk not a multiple of the 64-key tile (rows past Sk
+    read as zeros through the buffer bound), lengths 0, 1 and at tile
+    boundaries, Sq != Sk in both directions."""
+    q, _, _ = _qkv(4, 3, 400, 400, 64, tag=90)
+    _, k, v = _qkv(4, 3, Sk, Sk, 64, tag=95)
     lens = np.array(lens, np.int32)
     o = _run(dev, q, k, v, lens, torch.float16)
     assert np.all(o[lens == 0] == 0)

@@ -2,8 +2,9 @@
 //
 // fp16 path (MFMA). A workgroup of NW wavefronts owns NW*32 query rows of
 // one (batch, head); every wavefront owns 32 of them. Keys are walked in
-// tiles of 64: K and V are staged in LDS as [key][d] with 16-byte stores; the
-// V^T fragments of the P.V product come out of the transposing LDS read.
+// tiles of 64: K and V are staged in LDS as [key][d] with 16-byte stores (or
+// DMA'd there, fa_fwd_f16_ring_kernel); the V^T fragments of the P.V product
+// come out of the transposing LDS read.
 // The wavefront computes S^T = K . Q^T with 32x32x16 MFMAs, so each lane
 // ends up holding 32 keys of ONE query column (lane % 32): the row max and
 // row sum of the online softmax are then a register loop plus a single
@@ -141,6 +142,107 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_kernel(AttnParams p) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         if (PAD && dt * 32 + 8 * g + 4 * h32 >= p.D) continue;
+        f16x4 out;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out[j] = (f16)(o[dt][4 * g + j] * inv);
+        *(f16x4 *)(Ob + qrow * p.so[2] + dt * 32 + 8 * g + 4 * h32) = out;
+      }
+  }
+}
+
+// fp16, D = 64, key-padding lengths only (no boolean mask): the arithmetic
+// of fa_fwd_f16_kernel with 8 wavefronts of 32 queries, but K and V go
+// global -> LDS by DMA (buffer_load ... lds, 16 bytes per lane, nothing
+// staged in registers) into a ring of ST stages of one 64-key tile each
+// (8 KB of K, then 8 KB of V), so that up to ST - 1 tiles are in flight
+// while one is multiplied. One wavefront instruction moves 8 rows: wave w
+// fills rows 8w .. 8w + 7 of the K and of the V tile, lane l landing in
+// slot l % 8 of row 8w + l / 8, so it fetches the logical chunk whose
+// kv_swz slot that is. Keys at or beyond Sk lie past the buffer's end and
+// read as 0; keys in [valid length, Sk) are loaded and given probability 0,
+// as in fa_fwd_f16_kernel. The host launches it only when every byte offset
+// fits 31 bits. (A boolean mask is read from global memory inside the tile
+// loop, and that load could only be waited for together with the DMA of the
+// tiles in flight before it; fa_fwd_f16_kernel serves that case.)
+template <int ST>
+__global__ __launch_bounds__(512) void fa_fwd_f16_ring_kernel(AttnParams p) {
+  constexpr int D = 64, NW = 8, KT = 64, TILE = KT * D * 2;
+  __shared__ __attribute__((aligned(1024))) char ring[ST * 2 * TILE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h32 = lane >> 5;
+  const AttnTile tile = attn_tile();
+  const int b = tile.b, h = tile.h;
+  const int L = valid_len(p, b);
+  const f16 *Qb = (const f16 *)p.Q + b * p.sq[0] + h * p.sq[1];
+  const f16 *Kb = (const f16 *)p.K + b * p.sk[0] + h * p.sk[1];
+  const f16 *Vb = (const f16 *)p.V + b * p.sv[0] + h * p.sv[1];
+  f16 *Ob = (f16 *)p.O + b * p.so[0] + h * p.so[1];
+
+  const int qrow = tile.qb * (NW * 32) + wave * 32 + (lane & 31);
+  const bool qvalid = qrow < p.Sq;
+  f16x8 qf[D / 16];
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c)
+    qf[c] = qvalid ? *(const f16x8 *)(Qb + qrow * p.sq[2] + c * 16 + h32 * 8)
+                   : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  f32x16 o[D / 32];
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
+  float m = -__builtin_inff(), l = 0.f;
+
+  const int ntiles = (L + KT - 1) / KT;
+  const int rsk = (int)(p.sk[2] * 2), rsv = (int)(p.sv[2] * 2);  // row strides, bytes
+  const __amdgpu_buffer_rsrc_t rK = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)Kb, (short)0, (p.Sk - 1) * rsk + D * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rV = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)Vb, (short)0, (p.Sk - 1) * rsv + D * 2, 0x00020000);
+  const int trow = wave * 8 + (lane >> 3), chunk = (lane & 7) ^ kv_swz(trow);
+  const int offK = trow * rsk + chunk * 16, offV = trow * rsv + chunk * 16;
+  // Two instructions per tile and wavefront. The host compilation pass sees
+  // an empty statement (its check of this builtin with a run-time offset
+  // rejects the kernel).
+  auto issue = [&](int t, int stage) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    char *ks = ring + stage * 2 * TILE;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rK, ZK_LDS(ks + wave * 1024), 16,
+                                             offK + t * KT * rsk, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rV, ZK_LDS(ks + TILE + wave * 1024), 16,
+                                             offV + t * KT * rsv, 0, 0, 0);
+#else
+    (void)t, (void)stage;
+#endif
+  };
+#pragma unroll
+  for (int s = 0; s < ST; ++s)
+    if (s < ntiles) issue(s, s);
+  if (ntiles > 0) {
+    wait_slices<ST - 1, 2>(ntiles - 1);
+    lds_barrier();
+  }
+  int stage = 0;
+  for (int t = 0; t < ntiles; ++t) {
+    const char *ks = ring + stage * 2 * TILE;
+    attn32_tile<D, true, D, false>((const f16 *)ks, (const f16 *)(ks + TILE), qf, t, L,
+                                   p.scale_log2, &p, nullptr, lane, o, m, l);
+    if (t + 1 < ntiles) {
+      // tile t + 1 has landed (up to ST - 2 younger tiles still in flight),
+      // and after the barrier every wavefront is done reading tile t, whose
+      // stage then receives tile t + ST
+      wait_slices<ST - 2, 2>(ntiles - 2 - t);
+      lds_barrier();
+      if (t + ST < ntiles) issue(t + ST, stage);
+      stage = stage + 1 == ST ? 0 : stage + 1;
+    }
+  }
+
+  if (qvalid) {
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
         f16x4 out;
 #pragma unroll
         for (int j = 0; j < 4; ++j) out[j] = (f16)(o[dt][4 * g + j] * inv);
@@ -412,6 +514,10 @@ static void launch_f16_m(const AttnParams &p, hipStream_t s) {
       return;
     }
   }
+  // From 384 queries on, D = 64 with lengths only: the same shape with K and
+  // V DMA'd into a 3-stage ring (b32 s512, [B,H,S,D]: 43-45 -> 39.4-41.5 us,
+  // bit-identical output; 2 and 4 stages level; with the encoder's strided
+  // [B*S, 3H] layout level).
   // From 384 queries on (s512), 8 wavefronts (256 queries) per workgroup:
   // each staged K/V tile then serves twice the queries. The kernel is bound
   // by per-wave latency and occupancy (VALU 46% and matrix cores 19% busy at
@@ -420,6 +526,14 @@ static void launch_f16_m(const AttnParams &p, hipStream_t s) {
   // 32-query blocks per wavefront (half the LDS traffic per query, but 1-2
   // waves per SIMD) took 53-61 us. At 256 queries it would leave one
   // workgroup per (batch, head) and is slower (19.5 against 17.4 us).
+  if constexpr (D == 64 && !PAD && !MASK) {
+    const int64_t rs = 2 * (p.sk[2] > p.sv[2] ? p.sk[2] : p.sv[2]);
+    if (p.Sq >= 384 && rs >= 0 && ((int64_t)p.Sk + 64) * rs + 128 < (int64_t(1) << 31)) {
+      dim3 grid((unsigned)((p.Sq + 255) / 256), (unsigned)p.H, (unsigned)p.B);
+      fa_fwd_f16_ring_kernel<3><<<grid, 512, 0, s>>>(p);
+      return;
+    }
+  }
   if constexpr (D == 64) {
     if (p.Sq >= 384) {
       dim3 grid((unsigned)((p.Sq + 255) / 256), (unsigned)p.H, (unsigned)p.B);

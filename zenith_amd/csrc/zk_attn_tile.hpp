@@ -62,21 +62,16 @@ __device__ __forceinline__ int kv_swz(int r) {
   return ((r & 2) << 1) | ((r & 4) >> 1) | ((r >> 3) & 1);
 }
 
-// One 64-key tile of the 32-query wavefront (head dim D): scores S^T = K.Q^T
+// One 64-key tile of the 32-query wavefront (head dim D), in three phases
+// that attn32_tile runs in a row; a kernel may interleave the phases of
+// different wavefronts, each wavefront still running them in this order.
+// Phase 1, attn32_qk: scores S^T = K.Q^T of the tile's two 32-key blocks
 // from the K tile Kt (LDS, row pitch KLD halves, swizzled with kv_swz when
-// SWZ), keys >= L and (MASK) masked keys set to -inf, online-softmax update
-// of the running max m and sum l (lazy rescaling of o), then
-// O^T += V^T . P^T from the V tile Vt. t is the tile index (keys t*64 ..);
-// qf holds the wavefront's Q fragments. mp / mrow are read only with MASK.
-template <int D, bool SWZ, int KLD, bool MASK>
-__device__ __forceinline__ void attn32_tile(const f16 *Kt, const f16 *Vt, const f16x8 (&qf)[D / 16],
-                                            int t, int L, float scale_log2,
-                                            const AttnParams *mp, const uint8_t *mrow, int lane,
-                                            f32x16 (&o)[D / 32], float &m, float &l) {
-  constexpr int KT = 64;
+// SWZ); qf holds the wavefront's Q fragments.
+template <int D, bool SWZ, int KLD>
+__device__ __forceinline__ void attn32_qk(const f16 *__restrict__ Kt, const f16x8 (&qf)[D / 16],
+                                          int lane, f32x16 (&s)[2]) {
   const int h32 = lane >> 5;
-  // S^T[key][q] for the tile's two 32-key blocks.
-  f32x16 s[2];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -88,6 +83,19 @@ __device__ __forceinline__ void attn32_tile(const f16 *Kt, const f16 *Vt, const 
       s[kb] = mfma32x32x16(kf, qf[c], s[kb]);
     }
   }
+}
+
+// Phase 2, attn32_softmax: keys >= L and (MASK) masked keys set to -inf,
+// online-softmax update of the running max m and sum l (lazy rescaling of
+// o), and the probabilities as fp16 B fragments pf of the P.V product. t is
+// the tile index (keys t*64 ..); mp / mrow are read only with MASK.
+template <int D, bool MASK>
+__device__ __forceinline__ void attn32_softmax(f32x16 (&s)[2], int t, int L, float scale_log2,
+                                               const AttnParams *mp, const uint8_t *mrow,
+                                               int lane, f32x16 (&o)[D / 32], float &m,
+                                               float &l, f16x8 (&pf)[2][2]) {
+  constexpr int KT = 64;
+  const int h32 = lane >> 5;
   // Tile max on the raw scores (the scale is positive), masking only the
   // tile that straddles the valid length.
   const bool partial = t * KT + KT > L;
@@ -137,7 +145,6 @@ __device__ __forceinline__ void attn32_tile(const f16 *Kt, const f16 *Vt, const 
   // with m = -inf every score of this query is -inf so far: exp2 gives 0
   const float mneg = MASK && m == -__builtin_inff() ? 0.0f : -m;
   float psum = 0.f;
-  f16x8 pf[2][2];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -148,16 +155,21 @@ __device__ __forceinline__ void attn32_tile(const f16 *Kt, const f16 *Vt, const 
     }
   psum += __shfl_xor(psum, 32, 64);
   l += psum;
-  // O^T[d][q] += V^T[d][key] . P^T[key][q], 16 keys per MFMA. Lane-half
-  // h32, slot j of the P^T fragment holds key 16*c2 + 8*(j/4) + 4*h32 +
-  // j%4 of block kb; the V^T fragment (lane l: dim l % 32 of block dt, the
-  // same keys) comes from the row-major V tile through the transposing LDS
-  // read: in each group of 16 lanes, output lane i, slot j receives element
-  // i % 4 of the 4 elements read by source lane 4*j + i/4. Source lane s
-  // therefore reads key k0 + s/4, dims dbase + 4*(s%4), and output lane i
-  // gets dim dbase + i at keys k0 .. k0+3.
-  // (with SWZ: chunk ch of row r0 + 32 kb + 16 c2 sits in slot ch ^ kv_swz(r0),
-  // and of the row 8 further in slot ch ^ kv_swz(r0) ^ 1)
+}
+
+// Phase 3, attn32_pv: O^T[d][q] += V^T[d][key] . P^T[key][q] from the V
+// tile Vt, 16 keys per MFMA. Lane-half h32, slot j of the P^T fragment
+// holds key 16*c2 + 8*(j/4) + 4*h32 + j%4 of block kb; the V^T fragment
+// (lane l: dim l % 32 of block dt, the same keys) comes from the row-major V
+// tile through the transposing LDS read: in each group of 16 lanes, output
+// lane i, slot j receives element i % 4 of the 4 elements read by source
+// lane 4*j + i/4. Source lane s therefore reads key k0 + s/4, dims
+// dbase + 4*(s%4), and output lane i gets dim dbase + i at keys k0 .. k0+3.
+// (with SWZ: chunk ch of row r0 + 32 kb + 16 c2 sits in slot ch ^ kv_swz(r0),
+// and of the row 8 further in slot ch ^ kv_swz(r0) ^ 1)
+template <int D, bool SWZ, int KLD>
+__device__ __forceinline__ void attn32_pv(const f16 *__restrict__ Vt, const f16x8 (&pf)[2][2],
+                                          int lane, f32x16 (&o)[D / 32]) {
   const int grp = lane >> 4, sl = lane & 15;
   const int r0 = 4 * (grp >> 1) + (sl >> 2);
   const int fv = SWZ ? kv_swz(r0) : 0;
@@ -175,6 +187,24 @@ __device__ __forceinline__ void attn32_tile(const f16 *Kt, const f16 *Vt, const 
         const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         o[dt] = mfma32x32x16(vf, pf[kb][c2], o[dt]);
       }
+}
+
+// The three phases of one tile in a row (Kt, Vt: the tile's K and V).
+// Kt and Vt are restrict-qualified in every phase: the LDS reads through
+// them then carry alias information, without which the compiler makes each
+// transposing V read wait until every LDS DMA still in flight has landed
+// (the callers order their DMA themselves, by explicit waits and barriers).
+template <int D, bool SWZ, int KLD, bool MASK>
+__device__ __forceinline__ void attn32_tile(const f16 *__restrict__ Kt, const f16 *__restrict__ Vt,
+                                            const f16x8 (&qf)[D / 16], int t, int L,
+                                            float scale_log2, const AttnParams *mp,
+                                            const uint8_t *mrow, int lane, f32x16 (&o)[D / 32],
+                                            float &m, float &l) {
+  f32x16 s[2];
+  attn32_qk<D, SWZ, KLD>(Kt, qf, lane, s);
+  f16x8 pf[2][2];
+  attn32_softmax<D, MASK>(s, t, L, scale_log2, mp, mrow, lane, o, m, l, pf);
+  attn32_pv<D, SWZ, KLD>(Vt, pf, lane, o);
 }
 
 }  // namespace zk
