@@ -100,7 +100,9 @@ def load(path: str | None = None) -> ctypes.CDLL:
     with _lock:
         if _lib is not None and path is None:
             return _lib
-        p = path or LIB_PATH
+        # ZENITH_HIP_LIB names another build of the library (e.g. the
+        # host-sanitized one the CPU tests run the ABI checks against)
+        p = path or os.environ.get("ZENITH_HIP_LIB") or LIB_PATH
         if not os.path.exists(p):
             raise RuntimeError(
                 f"zenith_amd: HIP kernel library not found at {p}; build it with "
