@@ -890,7 +890,16 @@ static int forced_cfg() {
 static int pick_cfg(int M, int N, int K) {
   if (forced_cfg() >= 0) return forced_cfg();
   const int64_t tm256 = (M + 255) / 256;
-  if (M >= 1024 && N > 1024 && tm256 * ((N + 255) / 256) >= 256) return 0;
+  const int64_t t256 = tm256 * ((N + 255) / 256);
+  if (M >= 1024 && N > 1024 && t256 >= 256) {
+    // 256x256, unless 256x192 tiles take fewer whole rounds of 256 CUs times
+    // their area (units of 256x64): QKV at s512 (M = 16384, N = 2304) is 576
+    // tiles of 256x256, three rounds with the last a quarter full, or 768
+    // tiles of 256x192, three full rounds of smaller tiles
+    const int64_t t192n = tm256 * ((N + 191) / 192);
+    const int64_t c256 = (t256 + 255) / 256 * 4, c192 = (t192n + 255) / 256 * 3;
+    return c192 < c256 ? 5 : 0;
+  }
   // 256x192 tiles whenever they fill at least one wave of 256 CUs, also for
   // N <= 1024 at large M (s512: M = 16384, N = 768 gives exactly 256 tiles;
   // FFN-down 96.5 -> 73.6 us, out-projection 33.6 -> 24.2 us against the
