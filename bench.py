@@ -480,9 +480,13 @@ def measure_kernels(torch, dev, names=None):
         t = time_launches(torch, launch, n_iter=iters)
         scale = 1e12 if unit in ("TFLOP/s", "TOP/s") else 1e9
         ach = work / t / scale
-        out.append({"name": name, "shape": shape, "us": round(t * 1e6, 3), "bound": bound,
-                    "achieved": round(ach, 2), "unit": unit, "peak": PEAK[peak_key],
-                    "frac": round(ach / PEAK[peak_key], 4)})
+        row = {"name": name, "shape": shape, "us": round(t * 1e6, 3), "bound": bound,
+               "achieved": round(ach, 2), "unit": unit, "peak": PEAK[peak_key],
+               "frac": round(ach / PEAK[peak_key], 4)}
+        traffic = pmc_traffic(name)  # counter-measured HBM bytes per launch, if profiled
+        if traffic is not None:
+            row["traffic"] = traffic
+        out.append(row)
         del launch
         torch.cuda.empty_cache()
     return out
