@@ -614,17 +614,17 @@ def _host_info():
 
 
 def cpu_avx2_gemm():
-    """The reference's own CPU GEMM, matmul_f32_avx2 (core/src/cpu_kernels.cpp:
-    129-165, single-threaded i-k-j with 8-wide FMA), compiled from the
-    reference's source into oracle/_ref and timed on the config-2 BERT
-    shapes (M = 4096; one run each after a 256-row warm-up). Falls back to
-    the build's restatement (oracle/cpu_gemm.c) when oracle/_ref is absent."""
+    """The reference's CPU GEMM, matmul_f32_avx2 (core/src/cpu_kernels.cpp:
+    129-165, single-threaded i-k-j with 8-wide FMA), as this build restates
+    it in oracle/cpu_gemm.c (checked bit-identical to a build of the
+    reference's own source on the CPU side), timed on the config-2 BERT
+    shapes (M = 4096; one run each after a 256-row warm-up)."""
     import numpy as np
 
     from oracle import native
 
-    kind = "reference" if native.ref_available() else "port"
-    g = native.ref_gemm() if kind == "reference" else native.own_gemm()
+    kind = "port"
+    g = native.own_gemm()
     rows = []
     tot_f, tot_t = 0.0, 0.0
     for M, K, N, name in ((4096, 768, 2304, "qkv"), (4096, 768, 768, "out_proj"),

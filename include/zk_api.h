@@ -376,6 +376,9 @@ int zk_gemm_f16_ws(const void *A, const void *B, void *C, int64_t M, int64_t N,
  * products are split along K, their fp32 partials kept in a static 4 MiB
  * device array (one per GPU, held until the process ends; the split plan
  * never needs more, and a larger need is rejected with ZK_ERR_UNSUPPORTED).
+ * The first call on each device that splits looks up the array's address on
+ * that device (hipGetSymbolAddress) and must run outside graph capture; later
+ * calls make no HIP call besides their launches and can be captured.
  * Calls that overlap in time on one GPU race on that array. */
 int zk_gemm_f16_noalloc(const void *A, const void *B, void *C, int64_t M, int64_t N,
                         int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int trans_b,

@@ -24,7 +24,7 @@ def _split(t: np.ndarray, B: int, S: int, heads: int) -> np.ndarray:
 
 def bert_layer(x: np.ndarray, w: dict, lens: np.ndarray | None = None, heads: int = 12,
                eps: float = 1e-12, gelu: str = "erf", int8: dict | None = None,
-               act_f16: bool = False) -> np.ndarray:
+               act_f16: bool = False, taps: dict | None = None) -> np.ndarray:
     """x [B, S, H] float32 -> [B, S, H]. `int8`, if given, holds the INT8-FFN
     operands {Wi_q, s_wi, Wo2_q, s_wo2, s_x, s_h} and replaces the two FFN
     GEMMs by quantised ones (int32 accumulate, dequant + bias + GELU, then
@@ -33,7 +33,11 @@ def bert_layer(x: np.ndarray, w: dict, lens: np.ndarray | None = None, heads: in
     act_f16=True models a pipeline that stores every tensor passed between
     kernels in fp16 (fp32 arithmetic inside each op): each such tensor is
     rounded to fp16. With int8=None and act_f16=False this is the plain fp32
-    reference path."""
+    reference path.
+
+    taps, if given, receives the FFN input h1 [B*S, H] and the GELU output
+    u [B*S, FFN] (before any int8 quantisation): the activations whose
+    absmax calibrates the INT8 FFN's two activation scales."""
     B, S, H = x.shape
     st = (lambda t: t.astype(np.float16).astype(F32)) if act_f16 else (lambda t: t)
     x2 = st(x.reshape(B * S, H).astype(F32))
@@ -54,6 +58,8 @@ def bert_layer(x: np.ndarray, w: dict, lens: np.ndarray | None = None, heads: in
         u = st(ops.int8_linear(qh, int8["Wi_q"], int8["s_x"], int8["s_wi"], w["bi"], act))
         qu = ops.quantize_int8(u, int8["s_h"])
         d = st(ops.int8_linear(qu, int8["Wo2_q"], int8["s_h"], int8["s_wo2"], w["bo2"]))
+    if taps is not None:
+        taps["h1"], taps["u"] = h1, u
     out = st(ops.add_layernorm(d, h1, w["ln2_g"], w["ln2_b"], eps))
     return out.reshape(B, S, H)
 

@@ -181,9 +181,13 @@ def quantize_int8(x: np.ndarray, scale) -> np.ndarray:
     """q = clip(round_half_even(x / scale), -128, 127) in float32 arithmetic
     (quantize_to_int8 benchmarks/int8_bench.py:19-27: np.round is
     half-to-even; quantize_f32_to_int8_kernel core/src/cuda_kernels.cu:
-    918-937: __float2int_rn then clamp)."""
+    918-937: __float2int_rn then clamp). NaN gives 0: the reference kernel's
+    round-to-int conversion returns 0 for NaN before its clamp, and the
+    numpy rule's cast of the NaN that np.clip passes through gives 0 on x86
+    (a platform-defined cast, so it is written out here)."""
     x = x.astype(F32, copy=False)
     r = np.rint(x / F32(scale))
+    r = np.where(np.isnan(r), F32(0), r)
     return np.clip(r, -128, 127).astype(np.int8)
 
 

@@ -29,11 +29,16 @@ def _header_coefficients():
 
 
 def test_coefficients_are_the_fit():
+    """The header holds the fit's coefficients. A different scipy / HiGHS
+    release may land a coefficient one fp32 ulp away from the one in the
+    header, which the comparison allows; the accuracy the kernels rely on is
+    checked on the header's own coefficients below."""
     fit = _fit_module()
     coef, bound = fit.fit()
     hdr = _header_coefficients()
     assert hdr.shape == coef.shape == (fit.DEG + 1,)
-    assert np.array_equal(hdr, coef)
+    coef = np.asarray(coef, np.float32)
+    assert np.all(np.abs(hdr - coef) <= np.spacing(np.maximum(np.abs(hdr), np.abs(coef)))), (hdr, coef)
     assert hdr[-1] == -1.0          # Phi(0) = 1/2 exactly
     assert bound < 5e-7
 

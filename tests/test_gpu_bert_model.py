@@ -130,3 +130,46 @@ def test_bert_pooler_vs_transformers(dev, tmp_path):
     np.testing.assert_array_equal(m2.pool(m2(torch.from_numpy(ids))).float().cpu().numpy(), p)
     with pytest.raises(RuntimeError):
         BertModel.from_hf(_hf_model(layers=1), device=dev).pool(h)
+
+
+def _perturb_hf(hf, seed=42):
+    """In place: every LayerNorm gamma ~ 1 + N(0, 0.1), beta ~ N(0, 0.1), the
+    query biases ~ N(0, 0.5) and every other Linear bias ~ N(0, 0.05), drawn
+    per parameter (the distributions of synthetic.perturb_norms_and_biases),
+    instead of transformers' init (gamma 1, beta 0, biases 0 everywhere)."""
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for name, p in hf.named_parameters():
+            if name.endswith("LayerNorm.weight"):
+                p.copy_(1.0 + 0.1 * torch.randn(p.shape, generator=g))
+            elif name.endswith("LayerNorm.bias"):
+                p.copy_(0.1 * torch.randn(p.shape, generator=g))
+            elif name.endswith(".bias"):
+                std = 0.5 if ".query." in name else 0.05
+                p.copy_(std * torch.randn(p.shape, generator=g))
+    return hf
+
+
+def test_bert_model_wired_vs_transformers(dev):
+    """12 layers with per-layer LayerNorm parameters and non-zero biases
+    (the situation of a trained checkpoint), right-padded batch: the
+    encoder's LayerNorm folding and per-head bias interleave against
+    transformers' fp32 forward on the same weights, at the encoder bar."""
+    from zenith_amd.bert_model import BertModel
+
+    hf = _perturb_hf(_hf_model(layers=12, act="gelu", seed=6), seed=6)
+    B, S = 4, 128
+    rng = np.random.default_rng(7)
+    ids = rng.integers(0, 5000, (B, S)).astype(np.int64)
+    lens = synthetic.padding_lengths(B, S, seed=7)
+    mask = (np.arange(S)[None, :] < lens[:, None]).astype(np.int64)
+    with torch.no_grad():
+        ref = hf(input_ids=torch.from_numpy(ids),
+                 attention_mask=torch.from_numpy(mask)).last_hidden_state.numpy()
+    m = BertModel.from_hf(hf, device=dev)
+    assert m.encoder.folded(S)
+    y = m(torch.from_numpy(ids), attention_mask=torch.from_numpy(mask)).float().cpu().numpy()
+    rel = float(np.linalg.norm(y - ref) / np.linalg.norm(ref))
+    worst = float(np.max(np.abs(y - ref) - (2e-2 + 2e-2 * np.abs(ref))))
+    print(f"BertModel wired 12 layers vs transformers: rel {rel:.3e}, elementwise excess {worst:.3e}")
+    assert rel <= 2e-2 and worst <= 0, (rel, worst)

@@ -122,3 +122,57 @@ def test_dispatcher_fused_ops(dev):
     _check(ctx.get_tensor("f").float().cpu().numpy(), ref_f)
     assert d.get_dispatch_stats()["kernel_usage"] == {
         "hip_qkv_projection_fp16": 1, "hip_attention_epilogue_fp16": 1, "hip_ffn_fp16": 1}
+
+
+def test_torch_compile_transformers_bert(dev):
+    """The reference's own caller: torch.compile(transformers.BertModel,
+    backend="zenith") (zenith/adapters/pytorch_adapter.py:606-744, with the
+    SDPA rewrite of zenith/optimization/fx_patterns.py:81-114). A 12-layer
+    model with per-layer LayerNorm parameters and non-zero biases, in fp16
+    on the GPU, right-padded batch (transformers passes SDPA a boolean
+    [B, 1, S, S] mask and an explicit scale). dynamo captures one graph in
+    which every Linear, LayerNorm and SDPA node is a HIP leaf, and the output
+    matches transformers' fp32 CPU forward at the encoder bar."""
+    import copy
+
+    import torch._dynamo
+    import torch.nn.functional as F
+
+    from tests.test_gpu_bert_model import _hf_model, _perturb_hf
+    from zenith_amd.hooks import backend, fx_optimizer as O
+
+    nl = 12
+    hf = _hf_model(layers=nl, act="gelu", seed=8)
+    hf.config._attn_implementation = "sdpa"
+    _perturb_hf(hf, seed=8)
+    B, S = 4, 128
+    rng = np.random.default_rng(9)
+    ids = torch.from_numpy(rng.integers(0, 5000, (B, S)).astype(np.int64))
+    lens = synthetic.padding_lengths(B, S, seed=9)
+    mask = torch.from_numpy((np.arange(S)[None, :] < lens[:, None]).astype(np.int64))
+    with torch.no_grad():
+        ref = hf(input_ids=ids, attention_mask=mask).last_hidden_state.numpy()
+    m16 = copy.deepcopy(hf).half().to(dev).eval()
+    torch._dynamo.reset()
+    be = backend.register_backend("zenith")
+    cm = torch.compile(m16, backend="zenith", dynamic=False)
+    with torch.no_grad():
+        y = cm(input_ids=ids.to(dev), attention_mask=mask.to(dev)).last_hidden_state
+    y = y.float().cpu().numpy()
+    assert be.compiled_graphs == 1, be.compiled_graphs
+    gm = be.last_graph
+    left = [n for n in gm.graph.nodes if n.op == "call_function" and n.target in
+            (F.linear, F.layer_norm, F.scaled_dot_product_attention, F.gelu)]
+    left += [n for n in gm.graph.nodes if n.op == "call_module"
+             and isinstance(gm.get_submodule(n.target), (torch.nn.Linear, torch.nn.LayerNorm))]
+    assert not left, [n.format_node() for n in left]
+    t = O.replaced_targets(gm)
+    assert t.count("hip_linear") + t.count("hip_linear_gelu") == 6 * nl, t
+    assert t.count("hip_linear_gelu") == nl and t.count("hip_attention") == nl
+    assert t.count("hip_add_layernorm_eps") + t.count("hip_layernorm") == 2 * nl + 1
+    rel = float(np.linalg.norm(y - ref) / np.linalg.norm(ref))
+    worst = float(np.max(np.abs(y - ref) - (2e-2 + 2e-2 * np.abs(ref))))
+    print(f"torch.compile(transformers BertModel, backend='zenith'), {nl} layers: "
+          f"rel {rel:.3e}, elementwise excess {worst:.3e}")
+    assert rel <= 2e-2 and worst <= 0, (rel, worst)
+    torch._dynamo.reset()

@@ -171,13 +171,26 @@ def test_quantize_near_ties(dev, scale):
 def test_quantize_special_values(dev):
     """Saturation, signed zero and non-finite inputs through the 8-wide
     vector path (fp16 input) and the scalar path (fp32 input) alike: +-inf
-    and the largest fp16 values saturate, zeros give 0, NaN gives -128 (the
-    clamp returns its bound for NaN)."""
+    and the largest fp16 values saturate, zeros give 0, NaN gives 0 (the
+    reference's rule: its kernel's round-to-int conversion maps NaN to 0, and
+    its numpy rule's cast gives 0 on x86; tests/test_oracle.py pins the
+    oracle to that). Groups of eight with a NaN, with both infinities, and
+    with neither, so the vector path's careful branch and its fast branch
+    are both taken."""
     from zenith_amd import zenith_cuda as zc
 
     v = np.array([np.nan, np.inf, -np.inf, 65504.0, -65504.0, 0.0, -0.0, 1.0], np.float32)
-    want = np.array([-128, 127, -128, 127, -128, 0, 0, 25], np.int8)
-    x = np.tile(v, 64)
+    want = np.array([0, 127, -128, 127, -128, 0, 0, 25], np.int8)
+    clean = np.array([3.0, np.inf, -5.0, 65504.0, -65504.0, 0.0, -0.0, 1.0], np.float32)
+    want_clean = np.array([75, 127, -125, 127, -128, 0, 0, 25], np.int8)
+    nan_only = np.array([1.0, 2.0, np.nan, -1.0, 0.5, -0.5, 4.0, np.nan], np.float32)
+    x = np.concatenate([np.tile(v, 64), np.tile(clean, 64), np.tile(nan_only, 64)])
+    ref = np.concatenate([np.tile(want, 64), np.tile(want_clean, 64),
+                          np.tile(ops.quantize_int8(nan_only, np.float32(0.04)), 64)])
+    assert ref[128 * 8 + 2] == 0
     for dt in (torch.float16, torch.float32):
         q = zc.quantize_int8(torch.from_numpy(x).to(dev, dt), 0.04).cpu().numpy()
-        np.testing.assert_array_equal(q, np.tile(want, 64))
+        np.testing.assert_array_equal(q, ref)
+        np.testing.assert_array_equal(q, ops.quantize_int8(x.astype(np.float16).astype(np.float32)
+                                                           if dt == torch.float16 else x,
+                                                           np.float32(0.04)))

@@ -9,10 +9,12 @@ fallback (zenith/runtime/kernel_registry.py:118-153, tested in
 tests/test_numerical_accuracy.py:86-117), dispatcher marshalling
 (zenith/runtime/dispatcher.py:235-315)."""
 
+import warnings
+
+import pytest
 import torch
 import torch.fx
 import torch.nn.functional as F
-import pytest
 
 from zenith_amd.hooks import backend, fx_optimizer as O, fx_patterns as P
 from zenith_amd.hooks.dispatcher import (ExecutionContext, KernelDispatcher, Node,
@@ -242,9 +244,12 @@ def test_register_backend_replaces_an_existing_name():
         with pytest.raises(RuntimeError):
             backend.register_backend(name=name, replace=False)
         assert R.lookup_backend(name) is other
-        ours = backend.register_backend(name=name)
+        with pytest.warns(RuntimeWarning, match="replacing"):
+            ours = backend.register_backend(name=name)
         assert R.lookup_backend(name) is ours and ours is not other
-        ours2 = backend.register_backend(name=name)  # again: replaces our own
+        with warnings.catch_warnings():
+            warnings.simplefilter("error")  # replacing our own registration is silent
+            ours2 = backend.register_backend(name=name)
         assert R.lookup_backend(name) is ours2
     finally:
         R._COMPILER_FNS.pop(name, None)
@@ -363,3 +368,103 @@ def test_sdpa_mask_of_unknown_dtype_is_left_alone():
     gm = torch.fx.symbolic_trace(_MaskedSDPA())  # no shape metadata
     gm = O.FXOptimizer(require_gpu_inputs=False).optimize(gm, [])
     assert not any(n.op == "call_function" and n.target is P.hip_attention for n in gm.graph.nodes)
+
+
+class _LeafContracts:
+    """CPU stand-in for the zenith_cuda functions the FX leaves call: the
+    same argument contracts as zenith_amd/zenith_cuda.py (2-D rows and an
+    equal-shaped residual for add_layernorm, [N, K] weights for linear,
+    4-D Q/K/V and a boolean mask that broadcasts for flash_attention), the
+    arithmetic done by torch on the CPU, so that a rewritten graph can run
+    here and be compared with the graph it replaced."""
+
+    @staticmethod
+    def add_layernorm(input, residual, gamma, beta, eps=1e-5):
+        assert input.dim() == 2, "Input must be 2D [batch, hidden]"
+        assert residual is None or residual.shape == input.shape, "residual must match input"
+        assert gamma.numel() == beta.numel() == input.shape[1]
+        x = input if residual is None else input + residual
+        return F.layer_norm(x, (x.shape[1],), gamma, beta, eps)
+
+    @classmethod
+    def layernorm(cls, input, gamma, beta, eps=1e-5):
+        return cls.add_layernorm(input, None, gamma, beta, eps)
+
+    @staticmethod
+    def linear(x, weight, bias=None, activation=None, residual=None):
+        assert weight.dim() == 2 and x.shape[-1] == weight.shape[1]
+        y = F.linear(x, weight, bias)
+        return F.gelu(y) if activation == "gelu" else y
+
+    @staticmethod
+    def gelu(x, approximate="tanh"):
+        return F.gelu(x, approximate=approximate)
+
+    @staticmethod
+    def flash_attention(Q, K, V, key_padding_lengths=None, scale=None, attn_mask=None):
+        assert Q.dim() == K.dim() == V.dim() == 4 and K.shape == V.shape
+        assert Q.shape[-1] <= 128
+        if attn_mask is not None:
+            assert attn_mask.dtype == torch.bool
+            torch.broadcast_shapes(attn_mask.shape, (*Q.shape[:3], K.shape[2]))
+        return F.scaled_dot_product_attention(Q, K, V, attn_mask=attn_mask, scale=scale)
+
+
+def test_transformers_bert_graph_rewritten_to_hip_leaves(monkeypatch):
+    """What torch.compile hands the backend for a real transformers BertModel
+    (SDPA attention, right-padded batch: a boolean [B, 1, S, S] mask and an
+    explicit scale) is rewritten so that every Linear, LayerNorm and SDPA node
+    is a HIP leaf; run on the CPU through stand-ins that hold the leaves'
+    argument contracts, the rewritten graph gives the original graph's
+    output. (The embeddings' Add broadcasts a [1, S, H] position term, so it
+    stays a torch add in front of a plain LayerNorm leaf.)"""
+    import copy
+
+    transformers = pytest.importorskip("transformers")
+    import torch._dynamo
+
+    monkeypatch.setattr(P, "zenith_cuda", _LeafContracts)
+    torch.manual_seed(0)
+    nl = 2
+    cfg = transformers.BertConfig(hidden_size=768, num_attention_heads=12, intermediate_size=3072,
+                                  num_hidden_layers=nl, hidden_act="gelu", vocab_size=1000,
+                                  max_position_embeddings=128)
+    cfg._attn_implementation = "sdpa"
+    hf = transformers.BertModel(cfg, add_pooling_layer=False).eval()
+    with torch.no_grad():
+        for name, p in hf.named_parameters():  # non-trivial LayerNorms and biases
+            if name.endswith("LayerNorm.weight"):
+                p.copy_(1.0 + 0.1 * torch.randn(p.shape))
+            elif name.endswith(".bias"):
+                p.copy_(0.1 * torch.randn(p.shape))
+    seen = []
+
+    def recording_backend(gm, example_inputs):
+        opt = O.FXOptimizer(require_gpu_inputs=False, strict=True)
+        new = opt.optimize(copy.deepcopy(gm), example_inputs)
+        with torch.no_grad():
+            seen.append((new, gm(*example_inputs), new(*example_inputs)))
+        return gm.forward
+
+    ids = torch.randint(0, 1000, (2, 16))
+    mask = torch.ones(2, 16, dtype=torch.long)
+    mask[1, 9:] = 0
+    torch._dynamo.reset()
+    try:
+        with torch.no_grad():
+            torch.compile(hf, backend=recording_backend, dynamic=False)(input_ids=ids,
+                                                                         attention_mask=mask)
+    finally:
+        torch._dynamo.reset()
+    assert len(seen) == 1
+    gm, want, got = seen[0]
+    left = [n.format_node() for n in gm.graph.nodes if n.op == "call_function" and n.target in
+            (F.linear, F.layer_norm, F.scaled_dot_product_attention, F.gelu)]
+    assert not left, left
+    t = O.replaced_targets(gm)
+    assert t.count("hip_linear") + t.count("hip_linear_gelu") == 6 * nl
+    assert t.count("hip_linear_gelu") == nl and t.count("hip_attention") == nl
+    assert t.count("hip_add_layernorm_eps") == 2 * nl and t.count("hip_layernorm") == 1
+    want = want[0] if isinstance(want, (tuple, list)) else want
+    got = got[0] if isinstance(got, (tuple, list)) else got
+    torch.testing.assert_close(got, want, rtol=1e-4, atol=1e-4)

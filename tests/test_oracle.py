@@ -220,6 +220,19 @@ def test_quantize_rounding_and_clamp():
     np.testing.assert_array_equal(ops.quantize_int8(x, s), [0, 2, 0, -2, 2, 127, -128, 127, -128])
 
 
+def test_quantize_non_finite_matches_reference_rule():
+    """Non-finite inputs: the reference's numpy rule (benchmarks/int8_bench.py:
+    24, np.clip(np.round(x / scale), -128, 127).astype(np.int8)) as it runs
+    on this host gives 0 for NaN and saturates the infinities; the oracle
+    gives the same without relying on the platform-defined NaN cast."""
+    s = np.float32(0.04)
+    x = np.array([np.nan, -np.nan, np.inf, -np.inf, 0.0, -0.0, 1.0, -1.0], np.float32)
+    with np.errstate(invalid="ignore"):
+        rule = np.clip(np.round(x / s), -128, 127).astype(np.int8)
+    np.testing.assert_array_equal(rule, [0, 0, 127, -128, 0, 0, 25, -25])
+    np.testing.assert_array_equal(ops.quantize_int8(x, s), rule)
+
+
 def test_quantize_error_bound():
     x = synthetic.normal((100000,), tag=24) * 3
     s = ops.absmax_scale(np.abs(x).max())

@@ -59,3 +59,34 @@ def test_noalloc_argument_errors_match(dev):
     for args in ((16, 16, 16, 8, 8, 12, 12, 12, 8, 1, L.ZK_F16, None, None, 0, 0, None),
                  (16, 16, 16, 8, 8, 8, 4, 8, 8, 1, L.ZK_F16, None, None, 0, 0, None)):
         assert lib.zk_gemm_f16_noalloc(*args) == lib.zk_gemm_f16(*args) != 0
+
+
+def test_noalloc_under_graph_capture(dev):
+    """A split-K call captured into a HIP graph (torch.cuda.CUDAGraph) and
+    replayed: every replay is bit-identical to zk_gemm_f16_ws, also after an
+    eager call of another shape has overwritten the static array between
+    replays (each split writes its whole partial tile before the reduction
+    reads it, so nothing has to be cleared). The first call on a device
+    looks the array's device address up, which is done here eagerly, before
+    capture, as the header asks; after it a call makes no HIP API call
+    besides its two launches."""
+    lib = L.load()
+    M, K, N = 128, 3072, 768
+    need, c_ws, c_na, x, w, b = _gemm_pair(dev, M, K, N, L.ZK_EPI_BIAS, 40)
+    assert need > 0 and torch.equal(c_na, c_ws)
+    tx, tw, tb = (torch.from_numpy(a).to(dev, torch.float16) for a in (x, w, b))
+    out = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        st = lib.zk_gemm_f16_noalloc(tx.data_ptr(), tw.data_ptr(), out.data_ptr(), M, N, K, K, K,
+                                     N, 1, L.ZK_F16, tb.data_ptr(), None, 0, L.ZK_EPI_BIAS,
+                                     torch.cuda.current_stream().cuda_stream)
+    assert st == 0, L.last_error()
+    for i in range(3):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, c_ws), f"replay {i}"
+        # eager work between replays: a smaller split call on the same array
+        _, s_ws, s_na, *_ = _gemm_pair(dev, 64, 768, 768, L.ZK_EPI_BIAS_GELU_ERF, 50 + i)
+        assert torch.equal(s_na, s_ws)

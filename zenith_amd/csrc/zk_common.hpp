@@ -63,12 +63,15 @@ int gemm_f16_impl(const void *A, const void *B, void *C, int64_t M, int64_t N, i
 // unless t lies within 6e-5 of a half-integer; those values (about one in
 // ten thousand) take the IEEE division (hipcc keeps fp32 '/' correctly
 // rounded). For |t| >= 129 both forms saturate, whichever path is taken.
+// NaN gives 0, as in the reference: its kernel rounds with a float-to-int
+// conversion that turns NaN into 0 before the clamp, and its numpy rule
+// (benchmarks/int8_bench.py:24) casts the NaN left by np.clip to 0 on x86.
 __device__ __forceinline__ int8_t quant1(float x, float scale, float inv) {
   const float t = x * inv;
   float r = __builtin_rintf(t);
   if (fabsf(t - r) >= 0.49994f) r = __builtin_rintf(x / scale);
   r = fminf(fmaxf(r, -128.0f), 127.0f);
-  return (int8_t)(int)r;
+  return x != x ? (int8_t)0 : (int8_t)(int)r;
 }
 
 // Eight values at once, the same result as quant1 on each, packed as int8.
@@ -80,19 +83,23 @@ __device__ __forceinline__ int8_t quant1(float x, float scale, float inv) {
 // forms saturate. The offset makes every clamped value a byte in [0, 255]:
 // packed by v_cvt_pk_u8_f32 (exact on integers), then shifted back to
 // int8 by flipping each byte's top bit. The clamp is v_med3_f32, which
-// returns the minimum (0) when an operand is NaN: NaN gives -128, as in
-// quant1.
+// returns the minimum (0) when an operand is NaN, so a NaN must not reach
+// it: the sum of the eight t is NaN when one of them is (or when +inf and
+// -inf meet), and such a group takes the careful path too, where a NaN
+// becomes the byte 128, i.e. 0 as in quant1.
 __device__ __forceinline__ u32x2 quant8(const float (&x)[8], float scale, float inv) {
-  float r[8], dev = 0.f;
+  float r[8], dev = 0.f, sum = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float t = fmaf(x[e], inv, 128.0f);
     r[e] = __builtin_rintf(t);
     dev = fmaxf(dev, fabsf(t - r[e]));
+    sum += t;
   }
-  if (dev >= 0.49994f) {
+  if (dev >= 0.49994f || sum != sum) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) r[e] = __builtin_rintf(x[e] / scale) + 128.0f;
+    for (int e = 0; e < 8; ++e)
+      r[e] = x[e] != x[e] ? 128.0f : __builtin_rintf(x[e] / scale) + 128.0f;
   }
   uint32_t lo = 0, hi = 0;
 #pragma unroll

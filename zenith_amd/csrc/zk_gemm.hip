@@ -826,9 +826,12 @@ void gemm_mfma_kernel(GemmParams p) {
 // one wave's barrier or memory wait is covered by the other's MFMAs.
 constexpr int kNumCfgs = 6;
 
+// Returns false when no kernel of this configuration implements `epi` for
+// these operand types (nothing is launched then): callers turn that into
+// ZK_ERR_UNSUPPORTED instead of leaving the output unwritten.
 template <class OP, int BM, int BN, int MS, int BKB, int ST, typename OutT, bool DEQ, int WM = 2,
           int WN = 2>
-static void launch_epi(GemmParams p, int epi, hipStream_t s) {
+static bool launch_epi(GemmParams p, int epi, hipStream_t s) {
   p.tiles_n = (p.N + BN - 1) / BN;
   p.tiles_m = (p.M + BM - 1) / BM;
   const int grid = p.tiles_m * p.tiles_n * (p.splits > 1 ? p.splits : 1);
@@ -839,30 +842,31 @@ static void launch_epi(GemmParams p, int epi, hipStream_t s) {
   while (gm * 2 <= p.tiles_m && gm * gm * 4 <= per_xcd) gm *= 2;
   p.group_m = gm;
 #define ZK_L(E) \
-  gemm_mfma_kernel<OP, BM, BN, MS, BKB, ST, WM, WN, E, OutT, DEQ><<<grid, 64 * WM * WN, 0, s>>>(p)
+  (gemm_mfma_kernel<OP, BM, BN, MS, BKB, ST, WM, WN, E, OutT, DEQ><<<grid, 64 * WM * WN, 0, s>>>(p), \
+   true)
   switch (epi) {
-    case ZK_EPI_NONE: ZK_L(ZK_EPI_NONE); break;
-    case ZK_EPI_BIAS: ZK_L(ZK_EPI_BIAS); break;
-    case ZK_EPI_BIAS_GELU_ERF: ZK_L(ZK_EPI_BIAS_GELU_ERF); break;
-    case ZK_EPI_BIAS_GELU_TANH: ZK_L(ZK_EPI_BIAS_GELU_TANH); break;
+    case ZK_EPI_NONE: return ZK_L(ZK_EPI_NONE);
+    case ZK_EPI_BIAS: return ZK_L(ZK_EPI_BIAS);
+    case ZK_EPI_BIAS_GELU_ERF: return ZK_L(ZK_EPI_BIAS_GELU_ERF);
+    case ZK_EPI_BIAS_GELU_TANH: return ZK_L(ZK_EPI_BIAS_GELU_TANH);
     case ZK_EPI_BIAS_RESIDUAL:
-      if constexpr (!std::is_same<OutT, int8_t>::value) ZK_L(ZK_EPI_BIAS_RESIDUAL);
-      break;
-    case ZK_EPI_BIAS_RELU: ZK_L(ZK_EPI_BIAS_RELU); break;
+      if constexpr (!std::is_same<OutT, int8_t>::value) return ZK_L(ZK_EPI_BIAS_RESIDUAL);
+      return false;
+    case ZK_EPI_BIAS_RELU: return ZK_L(ZK_EPI_BIAS_RELU);
     default:
       // the folded-LayerNorm epilogues: fp16 in and out; statistics need
       // wave tiles of whole kLnSeg-column segments
       if constexpr (std::is_same<OP, F16Op>::value && std::is_same<OutT, f16>::value && !DEQ) {
-        if (epi == kEpiLnIn) ZK_L(kEpiLnIn);
-        if (epi == kEpiLnInGelu) ZK_L(kEpiLnInGelu);
+        if (epi == kEpiLnIn) return ZK_L(kEpiLnIn);
+        if (epi == kEpiLnInGelu) return ZK_L(kEpiLnInGelu);
         if constexpr ((BN / WN) % kLnSeg == 0)
-          if (epi == kEpiResStats) ZK_L(kEpiResStats);
+          if (epi == kEpiResStats) return ZK_L(kEpiResStats);
       }
       // the residual + statistics epilogue on the dequantised int8 product
       if constexpr (std::is_same<OP, I8Op>::value && std::is_same<OutT, f16>::value && DEQ &&
                     (BN / WN) % kLnSeg == 0)
-        if (epi == kEpiResStats) ZK_L(kEpiResStats);
-      break;
+        if (epi == kEpiResStats) return ZK_L(kEpiResStats);
+      return false;
   }
 #undef ZK_L
 }
@@ -877,14 +881,20 @@ static void launch_epi(GemmParams p, int epi, hipStream_t s) {
 //   M >= 1024 and >= 160 tiles of 256x192 (FFN-up: 256, QKV: 192): the
 //     8-wave 256x192 tile;
 //   otherwise 128x128 once that gives >= 640 tiles, else 128x96.
-// ZK_GEMM_CFG=<id> forces a configuration (tuning runs).
+// Tuning builds only (compiled with -DZK_TUNING): the environment variable
+// ZK_GEMM_CFG=<id> forces one configuration for every GEMM and turns split-K
+// off. The shipped library has no such switch and always plans by shape.
 static int forced_cfg() {
+#ifdef ZK_TUNING
   static int forced = -2;
   if (forced == -2) {
     const char *e = getenv("ZK_GEMM_CFG");
     forced = e ? atoi(e) : -1;
   }
   return forced >= 0 && forced < kNumCfgs ? forced : -1;
+#else
+  return -1;
+#endif
 }
 
 static int pick_cfg(int M, int N, int K) {
@@ -920,16 +930,24 @@ static int pick_cfg(int M, int N, int K) {
   return t128 >= 640 ? 1 : 2;
 }
 
+// Returns whether a kernel was launched (see launch_epi).
 template <class OP, typename OutT, bool DEQ>
-static void launch_mfma(GemmParams p, int epi, hipStream_t s, int cfg = -1) {
+[[nodiscard]] static bool launch_mfma(GemmParams p, int epi, hipStream_t s, int cfg = -1) {
   switch (cfg >= 0 ? cfg : pick_cfg(p.M, p.N, p.K)) {
-    case 0: launch_epi<OP, 256, 256, 32, 128, 2, OutT, DEQ, 2, 4>(p, epi, s); break;
-    case 1: launch_epi<OP, 128, 128, 32, 128, 2, OutT, DEQ>(p, epi, s); break;
-    case 2: launch_epi<OP, 128, 96, 16, 128, 2, OutT, DEQ>(p, epi, s); break;
-    case 4: launch_epi<OP, 128, 96, 32, 128, 3, OutT, DEQ, 4, 1>(p, epi, s); break;
-    case 5: launch_epi<OP, 256, 192, 32, 128, 2, OutT, DEQ, 4, 2>(p, epi, s); break;
-    default: launch_epi<OP, 64, 64, 16, 128, 2, OutT, DEQ>(p, epi, s); break;
+    case 0: return launch_epi<OP, 256, 256, 32, 128, 2, OutT, DEQ, 2, 4>(p, epi, s);
+    case 1: return launch_epi<OP, 128, 128, 32, 128, 2, OutT, DEQ>(p, epi, s);
+    case 2: return launch_epi<OP, 128, 96, 16, 128, 2, OutT, DEQ>(p, epi, s);
+    case 4: return launch_epi<OP, 128, 96, 32, 128, 3, OutT, DEQ, 4, 1>(p, epi, s);
+    case 5: return launch_epi<OP, 256, 192, 32, 128, 2, OutT, DEQ, 4, 2>(p, epi, s);
+    default: return launch_epi<OP, 64, 64, 16, 128, 2, OutT, DEQ>(p, epi, s);
   }
+}
+
+// The status of a GEMM entry point after launch_mfma: unsupported when no
+// kernel implements the epilogue for the chosen tile, else the launch check.
+static int launched(bool ok, const char *who, int epi) {
+  if (!ok) return fail(ZK_ERR_UNSUPPORTED, "%s: epilogue %d has no kernel for this shape", who, epi);
+  return check_launch(who);
 }
 
 // --------------------------------------------------------------- split-K --
@@ -983,8 +1001,16 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ w
 
 // p describes the final product (C, ldc, bias, residual); the partials go to
 // ws (at least split_ws_bytes). OP is F16Op or F32Op.
+// Returns whether both kernels were launched (false for an epilogue the
+// reduction does not implement; nothing is launched then).
 template <class OP, typename OutT>
-static void launch_split(GemmParams p, int epi, const SplitPlan &sp, float *ws, hipStream_t s) {
+[[nodiscard]] static bool launch_split(GemmParams p, int epi, const SplitPlan &sp, float *ws,
+                                       hipStream_t s) {
+  switch (epi) {
+    case ZK_EPI_NONE: case ZK_EPI_BIAS: case ZK_EPI_BIAS_GELU_ERF: case ZK_EPI_BIAS_GELU_TANH:
+    case ZK_EPI_BIAS_RESIDUAL: case ZK_EPI_BIAS_RELU: break;
+    default: return false;
+  }
   GemmParams q = p;
   q.C = ws;
   q.ldc = p.N;
@@ -993,7 +1019,7 @@ static void launch_split(GemmParams p, int epi, const SplitPlan &sp, float *ws, 
   q.splits = sp.splits;
   q.nk_per = sp.nk_per;
   q.split_stride = (int64_t)p.M * p.N;
-  launch_mfma<OP, float, false>(q, ZK_EPI_NONE, s, 3);
+  if (!launch_mfma<OP, float, false>(q, ZK_EPI_NONE, s, 3)) return false;
   const int64_t total = (int64_t)p.M * p.N;
   int64_t g = (total + 255) / 256;
   if (g > 4096) g = 4096;
@@ -1010,6 +1036,7 @@ static void launch_split(GemmParams p, int epi, const SplitPlan &sp, float *ws, 
     case ZK_EPI_BIAS_RELU: ZK_R(ZK_EPI_BIAS_RELU); break;
   }
 #undef ZK_R
+  return true;
 }
 
 // ------------------------------------------------------------- fp32 SIMT --
@@ -1122,15 +1149,16 @@ int zk::gemm_f16_impl(const void *A, const void *B, void *C, int64_t M, int64_t 
   GemmParams p{A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc, bias, residual, ldr, 1.f, nullptr, 0};
   hipStream_t s = as_stream(stream);
   const SplitPlan sp = plan_split(M, N, K, 2);
+  bool ok;
   if (ws && sp.splits > 1 && ws_bytes >= split_ws_bytes(M, N, sp) && aligned16(ws)) {
-    if (out_dtype == ZK_F16) launch_split<F16Op, f16>(p, epilogue, sp, (float *)ws, s);
-    else launch_split<F16Op, float>(p, epilogue, sp, (float *)ws, s);
+    if (out_dtype == ZK_F16) ok = launch_split<F16Op, f16>(p, epilogue, sp, (float *)ws, s);
+    else ok = launch_split<F16Op, float>(p, epilogue, sp, (float *)ws, s);
   } else if (out_dtype == ZK_F16) {
-    launch_mfma<F16Op, f16, false>(p, epilogue, s);
+    ok = launch_mfma<F16Op, f16, false>(p, epilogue, s);
   } else {
-    launch_mfma<F16Op, float, false>(p, epilogue, s);
+    ok = launch_mfma<F16Op, float, false>(p, epilogue, s);
   }
-  return check_launch("zk_gemm_f16");
+  return launched(ok, "zk_gemm_f16", epilogue);
 }
 
 extern "C" int zk_gemm_f16(const void *A, const void *B, void *C, int64_t M,
@@ -1273,9 +1301,9 @@ static int res_stats_run(const char *who, GemmParams p, const float *res_ln, con
   p.res_beta = res_beta;
   p.part_out = part_out;
   const int64_t t192 = (M + 255) / 256 * (N / 192);
-  launch_mfma<OP, f16, DEQ>(p, kEpiResStats, as_stream(stream),
-                            M >= 1024 && N % 192 == 0 && t192 >= 160 ? 5 : 4);
-  return check_launch(who);
+  const bool ok = launch_mfma<OP, f16, DEQ>(p, kEpiResStats, as_stream(stream),
+                                            M >= 1024 && N % 192 == 0 && t192 >= 160 ? 5 : 4);
+  return launched(ok, who, kEpiResStats);
 }
 
 extern "C" int zk_gemm_f16_res_stats(const void *A, const void *W, void *C, int64_t M, int64_t N,
@@ -1332,9 +1360,8 @@ extern "C" int zk_gemm_f16_ln(const void *A, const void *W, void *C, int64_t M, 
   p.ln_s = ln_s;
   p.ln_c = ln_c;
   p.ln_out = ln_out;
-  launch_mfma<F16Op, f16, false>(p, epilogue == ZK_EPI_BIAS ? kEpiLnIn : kEpiLnInGelu,
-                                 as_stream(stream));
-  return check_launch(who);
+  const int epi = epilogue == ZK_EPI_BIAS ? kEpiLnIn : kEpiLnInGelu;
+  return launched(launch_mfma<F16Op, f16, false>(p, epi, as_stream(stream)), who, epi);
 }
 
 // Shape / operand checks shared by the int8 entry points.
@@ -1370,8 +1397,8 @@ extern "C" int zk_gemm_i8(const int8_t *A, const int8_t *W, void *C, int64_t M,
   if (out_dtype == ZK_I32) {
     if (epilogue != ZK_EPI_NONE)
       return fail(ZK_ERR_INVALID, "zk_gemm_i8: int32 output takes no epilogue");
-    launch_mfma<I8Op, int32_t, false>(p, ZK_EPI_NONE, s);
-    return check_launch("zk_gemm_i8");
+    return launched(launch_mfma<I8Op, int32_t, false>(p, ZK_EPI_NONE, s), "zk_gemm_i8",
+                    ZK_EPI_NONE);
   }
   if (!s_w) return fail(ZK_ERR_INVALID, "zk_gemm_i8: dequantised output needs s_w");
   if (!(s_x > 0.f)) return fail(ZK_ERR_INVALID, "zk_gemm_i8: s_x must be > 0");
@@ -1379,10 +1406,11 @@ extern "C" int zk_gemm_i8(const int8_t *A, const int8_t *W, void *C, int64_t M,
     return fail(ZK_ERR_INVALID, "zk_gemm_i8: epilogue needs a bias");
   if (epilogue == ZK_EPI_BIAS_RESIDUAL && (!residual || ldr < N))
     return fail(ZK_ERR_INVALID, "zk_gemm_i8: residual epilogue needs residual and ldr >= N");
-  if (out_dtype == ZK_F16) launch_mfma<I8Op, f16, true>(p, epilogue, s);
-  else if (out_dtype == ZK_F32) launch_mfma<I8Op, float, true>(p, epilogue, s);
+  bool ok;
+  if (out_dtype == ZK_F16) ok = launch_mfma<I8Op, f16, true>(p, epilogue, s);
+  else if (out_dtype == ZK_F32) ok = launch_mfma<I8Op, float, true>(p, epilogue, s);
   else return fail(ZK_ERR_UNSUPPORTED, "zk_gemm_i8: out_dtype %d not supported", out_dtype);
-  return check_launch("zk_gemm_i8");
+  return launched(ok, "zk_gemm_i8", epilogue);
 }
 
 extern "C" int zk_gemm_i8_requant(const int8_t *A, const int8_t *W, int8_t *Q, int64_t M,
@@ -1401,8 +1429,8 @@ extern "C" int zk_gemm_i8_requant(const int8_t *A, const int8_t *W, int8_t *Q, i
     return fail(ZK_ERR_INVALID, "zk_gemm_i8_requant: epilogue needs a bias");
   GemmParams p{A, W, Q, (int)M, (int)N, (int)K, lda, ldw, ldq, bias, nullptr, 0, s_x, s_w, 0};
   p.s_q = s_out;
-  launch_mfma<I8Op, int8_t, true>(p, epilogue, as_stream(stream));
-  return check_launch("zk_gemm_i8_requant");
+  return launched(launch_mfma<I8Op, int8_t, true>(p, epilogue, as_stream(stream)),
+                  "zk_gemm_i8_requant", epilogue);
 }
 
 // Epilogue of the SIMT fp32 path, in place on C: the same operations, in the
@@ -1441,11 +1469,12 @@ static int gemm_f32_impl(const float *A, const float *B, float *C, int64_t M, in
       aligned16(B) && 255 * (lda + ldb) * 4 + 2 * K * 4 < 0x7ffffff0LL) {
     GemmParams p{A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc, bias, res, ldr, 1.f, nullptr, 0};
     const SplitPlan sp = plan_split(M, N, K, 4);
+    bool ok;
     if (ws && sp.splits > 1 && ws_bytes >= split_ws_bytes(M, N, sp) && aligned16(ws))
-      launch_split<F32Op, float>(p, epi, sp, (float *)ws, s);
+      ok = launch_split<F32Op, float>(p, epi, sp, (float *)ws, s);
     else
-      launch_mfma<F32Op, float, false>(p, epi, s);
-    return check_launch(who);
+      ok = launch_mfma<F32Op, float, false>(p, epi, s);
+    return launched(ok, who, epi);
   }
   if ((M + 63) / 64 > 65535) return fail(ZK_ERR_UNSUPPORTED, "zk_gemm_f32: M too large");
   dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));

@@ -408,6 +408,25 @@ class BertEncoder:
         self._run(x.contiguous().view(B * S, H), lengths, B, S, out, start, stop)
         return out.view(B, S, H)
 
+    def int8_ffn_tensors(self, layer: int) -> dict:
+        """After forward_layers(x, lengths, start, layer + 1) with the INT8 FFN,
+        the last layer's FFN tensors as it left them in the work buffers:
+        "h1" the FFN input (fp16, LN1's output), "q_h" its int8 copy, "q_u"
+        the re-quantised GELU output (int8), and "ffn_out" the FFN-down output
+        in fp16: dequantised + bias ("residual": False, unfolded layers), or
+        with the residual h1 added as well ("residual": True, folded layers,
+        whose next step is the LayerNorm of that sum)."""
+        if self.int8 is None or self._bufs is None:
+            raise RuntimeError("run forward_layers with the INT8 FFN first")
+        B, S = self._bufs["key"]
+        bf = self._bufs
+        if self.folded(S):
+            out = bf["ping"] if layer % 2 == 0 else bf["pong"]
+        else:
+            out = bf["t"]
+        return {"h1": bf["h1"], "q_h": bf["q_h"], "q_u": bf["q_u"], "ffn_out": out,
+                "residual": self.folded(S)}
+
     # --------------------------------------------------------- HIP graph ----
     def capture(self, B: int, S: int, with_lengths: bool = True):
         """Capture one forward at (B, S) into a HIP graph with static input /

@@ -21,6 +21,7 @@ generators on this path).
 from __future__ import annotations
 
 import logging
+import warnings
 from typing import Callable, Optional
 
 import torch
@@ -37,8 +38,10 @@ def create_compile_backend(target: str = "cuda", precision: str = "fp32",
     level = DEFAULT_OPT_LEVEL if opt_level is None else int(opt_level)
 
     def zenith_backend(gm: torch.fx.GraphModule, example_inputs: list):
+        zenith_backend.compiled_graphs += 1
         nodes = len(list(gm.graph.nodes))
         if level <= 1 or nodes < 10:
+            zenith_backend.last_graph = gm
             return gm.forward
         if level >= 2 and target.startswith("cuda"):
             opt = FXOptimizer(**kwargs)
@@ -47,10 +50,19 @@ def create_compile_backend(target: str = "cuda", precision: str = "fp32",
             logger.info("zenith_amd backend: %s", opt.get_stats())
         if precision == "fp16":
             gm = gm.half()
+        zenith_backend.last_graph = gm
         return gm.forward
 
+    # the statistics and the rewritten GraphModule of the last graph compiled,
+    # and how many graphs dynamo has handed over
     zenith_backend.last_stats = None
+    zenith_backend.last_graph = None
+    zenith_backend.compiled_graphs = 0
     return zenith_backend
+
+
+# backends this module registered, by name: replacing one of these is silent
+_REGISTERED: dict[str, Callable] = {}
 
 
 def register_backend(name: str = "zenith", replace: bool = True, **kwargs) -> Callable:
@@ -60,16 +72,28 @@ def register_backend(name: str = "zenith", replace: bool = True, **kwargs) -> Ca
     "zenith" (zenith/integrations/torch_dynamo.py:158-170), and dynamo
     refuses a second registration of a name. With replace=True (default) an
     existing registration of `name` is removed first, so
-    torch.compile(backend="zenith") reaches these kernels; with replace=False
-    a taken name raises RuntimeError instead of being silently kept."""
+    torch.compile(backend="zenith") reaches these kernels; a registration
+    this module did not make is replaced with a warning. With replace=False
+    a taken name raises RuntimeError instead of being silently kept.
+    Removing a registration uses dynamo's backend tables; a torch release
+    without them raises RuntimeError rather than guessing."""
     from torch._dynamo.backends import registry as _r
 
     backend = create_compile_backend(**kwargs)
-    taken = name in _r._COMPILER_FNS or name in _r.list_backends(exclude_tags=())
+    fns = getattr(_r, "_COMPILER_FNS", None)
+    taken = name in _r.list_backends(exclude_tags=()) or (fns is not None and name in fns)
     if taken:
         if not replace:
             raise RuntimeError(f"a torch.compile backend named {name!r} is already registered")
-        _r._COMPILER_FNS.pop(name, None)
-        _r._BACKENDS.pop(name, None)
+        if fns is None:
+            raise RuntimeError(f"cannot replace the torch.compile backend {name!r}: this torch "
+                               "release has no dynamo backend table to remove it from")
+        current = fns.get(name)
+        if current is None or current is not _REGISTERED.get(name):
+            warnings.warn(f"replacing the torch.compile backend registered as {name!r} "
+                          "with the zenith_amd HIP backend", RuntimeWarning, stacklevel=2)
+        fns.pop(name, None)
+        getattr(_r, "_BACKENDS", {}).pop(name, None)
     _r.register_backend(compiler_fn=backend, name=name)
+    _REGISTERED[name] = backend
     return backend

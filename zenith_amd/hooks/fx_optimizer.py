@@ -167,7 +167,8 @@ class FXOptimizer:
                     inp, w, b, eps = ln
                     if (inp.op == "call_function" and inp.target in _ADD and len(inp.users) == 1
                             and len(inp.args) == 2 and not inp.kwargs
-                            and all(isinstance(a, torch.fx.Node) for a in inp.args)):
+                            and all(isinstance(a, torch.fx.Node) for a in inp.args)
+                            and _same_shape(*inp.args)):
                         a0, a1 = inp.args
                         replace(node, P.hip_add_layernorm_eps, [a0, a1, w, b, eps])
                         g.erase_node(inp)
@@ -276,6 +277,24 @@ def _meta_last_dim(node):
             except (TypeError, ValueError):
                 return None
     return None
+
+
+def _meta_shape(node):
+    for key in ("val", "example_value", "tensor_meta"):
+        v = node.meta.get(key) if isinstance(node, torch.fx.Node) else None
+        shape = getattr(v, "shape", None)
+        if shape is not None:
+            return tuple(shape)
+    return None
+
+
+def _same_shape(a, b) -> bool:
+    """False when the graph's shape metadata shows a and b differ (an Add
+    that broadcasts, such as BERT's embeddings + [1, S, H] position term,
+    stays a torch add in front of the HIP LayerNorm); True when they agree
+    or the graph carries no metadata (the fused leaf broadcasts itself)."""
+    sa, sb = _meta_shape(a), _meta_shape(b)
+    return sa is None or sb is None or sa == sb
 
 
 def _meta_dtype(node):

@@ -183,6 +183,10 @@ def zenith_add_layernorm_replacement(x, residual, weight, bias):
 # forms with explicit eps / scale).
 @torch.fx.wrap
 def hip_add_layernorm_eps(x, residual, weight, bias, eps):
+    """LayerNorm(x + residual) over the last dimension; a residual that
+    broadcasts to x (a [1, S, H] position term, say) is expanded first."""
+    if residual.shape != x.shape:
+        residual = residual.expand(x.shape)
     return zenith_cuda.add_layernorm(_rows(x), _rows(residual), weight, bias, eps).view(x.shape)
 
 

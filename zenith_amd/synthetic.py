@@ -44,6 +44,43 @@ def bert_weights(num_layers: int = 12, hidden: int = 768, ffn: int = 3072,
     return [bert_layer_weights(rng, hidden, ffn) for _ in range(num_layers)]
 
 
+def perturb_norms_and_biases(layers: list[dict[str, np.ndarray]], seed: int = 42,
+                             g_std: float = 0.1, b_std: float = 0.1, bias_std: float = 0.05,
+                             q_bias_std: float = 0.5) -> list[dict[str, np.ndarray]]:
+    """Copies of `layers` with every LayerNorm gamma ~ 1 + N(0, g_std), beta
+    ~ N(0, b_std), the query bias ~ N(0, q_bias_std) and every other Linear
+    bias ~ N(0, bias_std), drawn per layer, so that no two layers share a
+    LayerNorm and no bias is zero (a trained checkpoint's situation). The
+    matrices are kept. Wiring mistakes that the default weights (gamma 1,
+    beta 0, biases 0 in every layer) cannot show, such as one layer's
+    LayerNorm applied in another layer, a dropped bias or beta term, or
+    Q/K/V biases interleaved differently from their weights, change the
+    output under these weights. The query bias is the larger one because a
+    key bias adds the same amount to every logit of a query and cancels in
+    the softmax: a query/key bias swap shows only through the query bias's
+    own effect on the logits, q_bias . k / sqrt(D)."""
+    rng = np.random.default_rng([seed, 3])
+    out = []
+    for w in layers:
+        w = dict(w)
+        for k in ("ln1_g", "ln2_g"):
+            w[k] = (1.0 + rng.standard_normal(w[k].shape) * g_std).astype(F32)
+        for k in ("ln1_b", "ln2_b"):
+            w[k] = (rng.standard_normal(w[k].shape) * b_std).astype(F32)
+        for k in ("bq", "bk", "bv", "bo", "bi", "bo2"):
+            std = q_bias_std if k == "bq" else bias_std
+            w[k] = (rng.standard_normal(w[k].shape) * std).astype(F32)
+        out.append(w)
+    return out
+
+
+def bert_weights_wired(num_layers: int = 12, hidden: int = 768, ffn: int = 3072,
+                       seed: int = 42) -> list[dict[str, np.ndarray]]:
+    """bert_weights with per-layer LayerNorm parameters and non-zero biases
+    (perturb_norms_and_biases): the weight set of the composition tests."""
+    return perturb_norms_and_biases(bert_weights(num_layers, hidden, ffn, seed), seed)
+
+
 def hidden_states(batch: int, seq: int, hidden: int = 768, seed: int = 42) -> np.ndarray:
     """Token embeddings ~ N(0, 1), [batch, seq, hidden] float32."""
     rng = np.random.default_rng([seed, 1])
