@@ -69,6 +69,7 @@ def _args():
     ap.add_argument("--no-kernels", action="store_true")
     ap.add_argument("--no-e4", action="store_true", help="skip the hybrid-API encoder (E4)")
     ap.add_argument("--no-s512", action="store_true", help="skip the seq-512 encoder line")
+    ap.add_argument("--no-small", action="store_true", help="skip the b1 / b4 encoder lines")
     ap.add_argument("--only", default=None, help="launch one kernel --iters times and exit")
     ap.add_argument("--iters", type=int, default=20)
     return ap.parse_args()
@@ -447,6 +448,26 @@ def kernel_cases(torch, dev):
         "copy": copy(),
     }
 
+def _attn_computed_flops(S, B=32, heads=12, D=64, proj=0.0):
+    """FLOPs the attention kernels do with the benchmark's key-padding lengths:
+    every query row against ceil(L_b / 64) 64-key tiles of its sequence (the
+    tiles past L_b are skipped), QK^T and PV, 4 D flops per (query, key) per
+    head; plus `proj` (the fused QKV projection's GEMM FLOPs)."""
+    from zenith_amd import synthetic
+
+    lens = synthetic.padding_lengths(B, S)
+    keys = sum(min(S, -(-int(L) // 64) * 64) for L in lens)
+    return proj + 4.0 * heads * D * S * keys
+
+
+_QKV_FLOPS = 2.0 * 32 * 128 * 3 * 768 * 768
+ATTN_COMPUTED = {
+    "attn_s128": lambda: _attn_computed_flops(128),
+    "attn_s512": lambda: _attn_computed_flops(512),
+    "qkv_attn_s128": lambda: _attn_computed_flops(128, proj=_QKV_FLOPS),
+    "qkv_attn_ln_s128": lambda: _attn_computed_flops(128, proj=_QKV_FLOPS),
+}
+
 # kernels one step of the timed encoder (b32 s128) launches, per layer: the
 # roofline line names the longest of them
 STEP_KERNELS = ("qkv_attn_ln_s128", "out_proj_res_stats", "ffn_up_ln", "ffn_down_res_stats")
@@ -469,6 +490,47 @@ KERNEL_DESC = {
 }
 
 
+def confirm_peaks(torch, dev):
+    """The MI355X peaks the roofline fractions divide by, confirmed on this
+    box: CU count (device properties), maximum shader clock (HIP attribute),
+    the clock under sustained MFMA load (zk_clock_probe: every CU's SIMDs
+    kept busy with independent fp16 MFMAs, shader cycles over wall time) and
+    the fp16 dense peak that clock gives (256 CUs x 4096 FLOP per clock at
+    2.4 GHz is the 2.5 PFLOP/s datasheet figure), and a 256 MB + 256 MB copy's
+    bandwidth against the 8 TB/s datasheet HBM figure."""
+    import ctypes
+
+    import numpy as np
+
+    from zenith_amd import _lib as L
+
+    lib = L.load()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    out = torch.zeros(2 * cus, dtype=torch.int64, device=dev)
+    khz = (ctypes.c_int64 * 2)()
+    stream = torch.cuda.current_stream().cuda_stream
+    ghz = []
+    for n in (2000, 20000, 20000):  # the first run warms up
+        _rc(L, lib.zk_clock_probe(cus, n, out.data_ptr(), khz, stream))
+        torch.cuda.synchronize()
+        t = out.cpu().numpy().reshape(cus, 2).astype(np.float64)
+        ghz.append(float(np.mean(t[:, 0] / (t[:, 1] / (khz[0] * 1e3))) / 1e9))
+    clk = min(ghz[1:])
+    launch, work = kernel_cases(torch, dev)["copy"]()[:2]
+    t_copy = time_launches(torch, launch, n_iter=20)
+    del launch
+    torch.cuda.empty_cache()
+    copy_gbs = work / t_copy / 1e9
+    return {"cu_count": cus, "max_sclk_mhz": round(khz[1] / 1e3, 1),
+            "mfma_sustained_clock_ghz": round(clk, 3),
+            "fp16_dense_tflops_at_sustained_clock": round(cus * 4096 * clk / 1e3, 1),
+            "fp16_dense_tflops_datasheet": PEAK["fp16"],
+            "hbm_copy_gbs_measured": round(copy_gbs, 1), "hbm_gbs_datasheet": PEAK["hbm"],
+            "method": "zk_clock_probe: one 8-wave workgroup per CU, four independent 32x32x16 "
+                      "fp16 MFMA chains per wave, shader clock64 over wall_clock64; copy: "
+                      "256 MB read + 256 MB write (zk_relu fp16), HIP events, 20 launches"}
+
+
 def measure_kernels(torch, dev, names=None):
     out = []
     cases = kernel_cases(torch, dev)
@@ -483,6 +545,16 @@ def measure_kernels(torch, dev, names=None):
         row = {"name": name, "shape": shape, "us": round(t * 1e6, 3), "bound": bound,
                "achieved": round(ach, 2), "unit": unit, "peak": PEAK[peak_key],
                "frac": round(ach / PEAK[peak_key], 4)}
+        computed = ATTN_COMPUTED.get(name)
+        if computed is not None:
+            # the dense count (the reference's formula) is `achieved`; the
+            # kernels skip the key tiles past each valid length, so the work
+            # they do is smaller: both are reported
+            w2 = computed()
+            row["work_dense"] = work
+            row["work_computed"] = w2
+            row["achieved_computed"] = round(w2 / t / scale, 2)
+            row["frac_computed"] = round(w2 / t / scale / PEAK[peak_key], 4)
         traffic = pmc_traffic(name)  # counter-measured HBM bytes per launch, if profiled
         if traffic is not None:
             row["traffic"] = traffic
@@ -557,6 +629,47 @@ def e4_hybrid(torch, runs: int = 50, warmup: int = 5):
             "seqs_per_s": round(1e3 / ms, 1), "published_ms": E4_PUBLISHED_MS,
             "published_hw": "T4", "vs_published": round(E4_PUBLISHED_MS / ms, 2),
             "ms_graph_replay": round(ms_g, 3), "vs_published_graph_replay": round(E4_PUBLISHED_MS / ms_g, 2)}
+
+
+def small_batch_lines(torch, dev, layers, args, S=128):
+    """The fp16 encoder at b1 and b4 (seq 128, key-padding lengths, HIP-graph
+    replay), through the small-batch path (unfolded layers, 64x64 tiles with
+    split-K, one-wavefront attention workgroups). b1 is the reference's own
+    BERT benchmark shape: its published b1 s128 figures on a T4 are 9.74 ms
+    (hybrid mode) and 10.60 ms (PyTorch), BENCHMARK_REPORT.md:47-59, and its
+    tutorial's expected fp16 figure 4.80 ms (docs/tutorial/
+    11_full_performance.md:174-178)."""
+    from zenith_amd import synthetic
+    from zenith_amd.encoder import BertEncoder
+
+    out = {}
+    for B in (1, 4):
+        _log(f"small-batch encoder b{B} s{S}")
+        enc = BertEncoder(layers, device=dev)
+        gx, gl, go = enc.capture(B, S)
+        gx.copy_(torch.from_numpy(synthetic.hidden_states(B, S, seed=44)).to(dev, torch.float16))
+        gl.copy_(torch.from_numpy(synthetic.padding_lengths(B, S, seed=44)).to(dev))
+        steps = args.steps
+        for _ in range(args.warmup):
+            enc.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            enc.replay()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        assert torch.isfinite(go.float()).all(), f"non-finite encoder output (b{B})"
+        ms = dt / steps * 1e3
+        line = {"value": round(B * steps / dt, 2), "unit": "seqs/s", "batch": B, "seq_len": S,
+                "steps": steps, "ms_per_step": round(ms, 4),
+                "path": "small batch" if enc.small_batch(B, S) else "folded"}
+        if B == 1:
+            line.update({"published_ms": {"hybrid_T4": E4_PUBLISHED_MS, "pytorch_T4": 10.60,
+                                          "expected_fp16_T4": 4.80},
+                         "vs_published_hybrid": round(E4_PUBLISHED_MS / ms, 2)})
+        out[f"b{B}"] = line
+        del enc
+    return out
 
 
 # ---------------------------------------------------------- CPU baseline --
@@ -780,11 +893,16 @@ def main():
             s512["int8_ffn"] = {"value": round(B * steps2 / dt28, 2),
                                 "ms_per_step": round(dt28 / steps2 * 1e3, 4)}
             enc.disable_int8_ffn()
+    # one and four sequences (the reference's b1 s128 BERT benchmark, and one
+    # rank's share of b32 over eight GPUs): the small-batch path
+    small = None if args.no_small else small_batch_lines(torch, dev, layers, args)
     del enc
     torch.cuda.empty_cache()
 
     _log("E4 hybrid encoder")
     e4 = None if args.no_e4 else e4_hybrid(torch)
+    _log("peaks")
+    peaks = confirm_peaks(torch, dev)
     _log("kernel table")
     kernels = measure_kernels(torch, dev, None if not args.no_kernels else STEP_KERNELS)
     # the roofline line is the step's dominant kernel: the longest of the
@@ -804,9 +922,11 @@ def main():
         "encoder_tflops": round(fwd_flops * args.steps / dt / 1e12, 2),
         "int8_ffn": int8,
         "encoder_s512": s512,
+        "encoder_small_batch": small,
         "roofline": {"bound": roof["bound"], "achieved": roof["achieved"], "peak": roof["peak"],
                      "unit": roof["unit"], "frac": roof["frac"],
                      "traffic": pmc_traffic(roof["name"])},
+        "peaks": peaks,
         "roofline_kernel": {"name": roof["name"], "kernel": KERNEL_DESC[roof["name"]],
                             "avg_launch_us": roof["us"],
                             "per_step_candidates_us": {k["name"]: k["us"] for k in kernels

@@ -54,6 +54,15 @@ typedef enum {
 const char *zk_last_error(void);
 int zk_version(void);
 
+/* Measurement aid, no counterpart in the reference: the shader clock under
+ * sustained matrix-core load, with which the benchmark confirms the peak its
+ * roofline fractions divide by. `grid` workgroups of eight wavefronts each
+ * run 4 x n_mfma independent 32x32x16 fp16 MFMAs; out (device, int64
+ * [grid][2]) receives each workgroup's shader-clock cycles and wall-clock
+ * ticks, khz (host, int64 [2]) the wall clock's rate and the device's
+ * maximum shader clock, in kHz. */
+int zk_clock_probe(int grid, int n_mfma, int64_t *out, int64_t *khz, void *stream);
+
 /* y = max(x, 0), n elements, dtype ZK_F32 or ZK_F16. x may equal y.
  * Replaces zenith_cuda.relu: core/bindings/cuda_bindings.cpp:39-46 ->
  * relu_f32 core/src/cuda_kernels.cu:504-507. */

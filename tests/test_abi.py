@@ -31,6 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 
 @pytest.mark.parametrize("call,code", [
+    (lambda lib: lib.zk_clock_probe(0, 10, None, None, None), L.ZK_ERR_INVALID),
     (lambda lib: lib.zk_relu(None, None, -1, L.ZK_F32, None), L.ZK_ERR_INVALID),
     (lambda lib: lib.zk_relu(None, None, 5, L.ZK_F32, None), L.ZK_ERR_INVALID),
     (lambda lib: lib.zk_relu(1, 1, 5, 7, None), L.ZK_ERR_UNSUPPORTED),

@@ -158,7 +158,7 @@ def test_bert_model_wired_vs_transformers(dev):
     from zenith_amd.bert_model import BertModel
 
     hf = _perturb_hf(_hf_model(layers=12, act="gelu", seed=6), seed=6)
-    B, S = 4, 128
+    B, S = 16, 128  # 2048 rows: the folded layers (fewer rows run unfolded)
     rng = np.random.default_rng(7)
     ids = rng.integers(0, 5000, (B, S)).astype(np.int64)
     lens = synthetic.padding_lengths(B, S, seed=7)
@@ -167,7 +167,7 @@ def test_bert_model_wired_vs_transformers(dev):
         ref = hf(input_ids=torch.from_numpy(ids),
                  attention_mask=torch.from_numpy(mask)).last_hidden_state.numpy()
     m = BertModel.from_hf(hf, device=dev)
-    assert m.encoder.folded(S)
+    assert m.encoder.folded(S, B)
     y = m(torch.from_numpy(ids), attention_mask=torch.from_numpy(mask)).float().cpu().numpy()
     rel = float(np.linalg.norm(y - ref) / np.linalg.norm(ref))
     worst = float(np.max(np.abs(y - ref) - (2e-2 + 2e-2 * np.abs(ref))))

@@ -85,6 +85,37 @@ def test_config5_encoder_fp16(dev, kind, S, fused, fold):
           f"({len(pick)} sequences), vs fp16-storage oracle {rel16:.3e}")
 
 
+@pytest.mark.parametrize("B", [1, 4])
+def test_small_batch_encoder(dev, B):
+    """One and four sequences of 128 tokens (the reference's own BERT
+    benchmark shape, and one rank's share of a batch of 32 over eight GPUs):
+    the small-batch path (unfolded layers, 64x64 GEMM tiles with split-K
+    through a workspace, one-wavefront attention workgroups) on the wired
+    weights, every sequence against the fp32 oracle at the encoder bar; a
+    HIP-graph replay gives the eager output bit for bit."""
+    from zenith_amd.encoder import BertEncoder
+
+    S = 128
+    w = _weights("wired")
+    x = synthetic.round_f16(synthetic.hidden_states(B, S, seed=5))
+    lens = synthetic.padding_lengths(B, S, seed=5)
+    enc = BertEncoder(w, device=dev)
+    assert enc.small_batch(B, S) and not enc.folded(S, B) and not enc.fused_attention(S, B)
+    xt = torch.from_numpy(x).to(dev, torch.float16)
+    lt = torch.from_numpy(lens).to(dev)
+    y = enc(xt, lt)
+    assert enc._bufs["ws"] is not None  # some product is split at this size
+    yn = y.float().cpu().numpy()
+    rel = _check(yn, obert.bert_encoder(x, w, lens))
+    gx, gl, go = enc.capture(B, S)
+    gx.copy_(xt)
+    gl.copy_(lt)
+    enc.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(go, y)
+    print(f"small-batch encoder b{B} s{S}: rel vs fp32 oracle {rel:.3e}")
+
+
 @pytest.mark.parametrize("S,int8", [(128, False), (512, False), (128, True), (512, True)])
 def test_config5_batch_permutation_invariance(dev, S, int8):
     """The B=32 batch run in reversed order gives every sequence's output

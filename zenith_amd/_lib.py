@@ -38,6 +38,7 @@ _f32 = ctypes.c_float
 SIGNATURES: dict[str, list] = {
     "zk_last_error": [],
     "zk_version": [],
+    "zk_clock_probe": [_i32, _i32, _vp, _vp, _vp],
     "zk_relu": [_vp, _vp, _i64, _i32, _vp],
     "zk_sigmoid": [_vp, _vp, _i64, _i32, _vp],
     "zk_tanh": [_vp, _vp, _i64, _i32, _vp],

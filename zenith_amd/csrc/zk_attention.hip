@@ -508,7 +508,16 @@ static void launch_f16_m(const AttnParams &p, hipStream_t s) {
       // one 64-key tile per LDS stage, the next one loading under the
       // current one's MFMAs. Staging both tiles of a 128-key sequence at once
       // (TPS = 2) was 0.7% slower per encoder step, fp16 and INT8-FFN, in
-      // both-order A/Bs on two boxes.
+      // both-order A/Bs on two boxes. A few (batch, head) pairs (one to
+      // four 128-token sequences: 96 to 384 workgroups of one wavefront
+      // instead of 24 to 96 of four) take one wavefront per workgroup, so
+      // that more CUs share the work.
+      const unsigned bh = (unsigned)p.H * (unsigned)p.B;
+      if ((unsigned)((p.Sq + 63) / 64) * bh < 256) {
+        dim3 grid((unsigned)((p.Sq + 15) / 16), (unsigned)p.H, (unsigned)p.B);
+        fa_fwd_f16_q16_kernel<1, 1, MASK><<<grid, 64, 0, s>>>(p);
+        return;
+      }
       dim3 grid((unsigned)((p.Sq + 63) / 64), (unsigned)p.H, (unsigned)p.B);
       fa_fwd_f16_q16_kernel<4, 1, MASK><<<grid, 256, 0, s>>>(p);
       return;

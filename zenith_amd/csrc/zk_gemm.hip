@@ -924,6 +924,13 @@ static int pick_cfg(int M, int N, int K) {
   // faster on 64x64 than on the 128x128 ring (16.3 against 18.0 us), but
   // inside the encoder the ring won (1.212 against 1.234 ms per step), so
   // encoder figures decide.
+  // Below 1024 rows (a few sequences: the per-GPU share of a data-parallel
+  // batch, or serving) the 64x64 tile whenever the larger ones would leave
+  // CUs idle: at M = 512 (four 128-token sequences) the QKV projection is 96
+  // tiles of 128x96 or 288 of 64x64, FFN-down 32 tiles of 128x96 or 96 of
+  // 64x64 (which split-K then doubles when a workspace is given).
+  const int64_t t96 = (int64_t)((M + 127) / 128) * ((N + 95) / 96);
+  if (M < 1024 && t96 < 256) return 3;
   if (N <= 1024) return K >= 2048 ? 4 : 3;
   if (M >= 1024 && t192 >= 160) return 5;
   const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);

@@ -230,7 +230,12 @@ static int ln_impl(const void *xv, const void *rv, const void *gv,
     // fp16), else a whole wavefront per row.
 #define ZK_LN(MV, LPR) \
   ln_wave_launch<T, MV, LPR, Q8>(x, r, g, b, y, q, qs, rows, h, eps, post, rl, s)
-    if (nvec <= 32) ZK_LN(1, 32);
+    // With few rows (under 2048: a few sequences) a whole wavefront per row
+    // gives four rows per workgroup instead of eight, twice the workgroups.
+    const bool few = rows < 2048;
+    if (few && nvec <= 64) ZK_LN(1, 64);
+    else if (few && nvec <= 128) ZK_LN(2, 64);
+    else if (nvec <= 32) ZK_LN(1, 32);
     else if (nvec <= 64) ZK_LN(2, 32);
     else if (nvec <= 96) ZK_LN(3, 32);
     else if (nvec <= 128) ZK_LN(4, 32);

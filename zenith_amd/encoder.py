@@ -41,6 +41,12 @@ from . import _lib as L
 
 F16 = torch.float16
 
+# Rows (batch x seq) below which a forward runs as a small batch (see
+# BertEncoder.small_batch). Measured per step at s128 (12 layers, HIP-graph
+# replay), folded against small-batch path: b1 0.835 / 0.606 ms, b2 0.924 /
+# 0.642, b4 0.945 / 0.757, b8 1.000 / 0.962, b16 1.025 / 1.033.
+SPLIT_ROWS = 2048
+
 
 def _dev(a: np.ndarray, dtype, device) -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(a)).to(device=device, dtype=dtype)
@@ -81,7 +87,8 @@ class BertEncoder:
 
     def __init__(self, layers: list[dict], heads: int = 12, eps: float = 1e-12,
                  gelu: str = "erf", device: str | torch.device = "cuda",
-                 fuse_qkv_attention: bool = True, fold_layernorm: bool = True):
+                 fuse_qkv_attention: bool = True, fold_layernorm: bool = True,
+                 split_rows: int = SPLIT_ROWS):
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise RuntimeError("BertEncoder runs on a GPU device")
@@ -95,6 +102,9 @@ class BertEncoder:
             raise RuntimeError("hidden size must be a multiple of heads")
         self.head_dim = self.hidden // heads
         self.fuse_qkv_attention = bool(fuse_qkv_attention)
+        # below this many rows (batch x seq) the layers run unfolded, with
+        # split-K GEMMs through a workspace (see _buffers and small_batch)
+        self.split_rows = int(split_rows)
         # LayerNorms folded into the GEMMs that consume them (fp16 FFN, erf
         # GELU, hidden size a multiple of 96 up to 1536: the row statistics
         # travel as (mean, M2) of 96-column segments)
@@ -142,12 +152,24 @@ class BertEncoder:
             out.update({"Wqkv_f": _dev(wq, F16, d), "s_qkv": f32(sq), "c_qkv": f32(cq)})
         return out
 
-    def fused_attention(self, S: int) -> bool:
-        """Whether sequences of S tokens take the fused QKV + attention
-        launch (zk_qkv_attn_f16: S of 64 or 128, head_dim 64)."""
-        return self.fuse_qkv_attention and S in (64, 128) and self.head_dim == 64
+    def small_batch(self, B: int | None, S: int) -> bool:
+        """Whether B sequences of S tokens (B*S rows) run as a small batch:
+        the fused and folded kernels tile 128 or 256 rows at a time, so a few
+        sequences leave most CUs idle (b4 s128: 24 to 32 workgroups per
+        launch on 256 CUs); below split_rows rows the layers run unfolded,
+        with 64x64 GEMM tiles, split-K through a workspace where even those
+        are too few, and the separate attention and Add+LayerNorm kernels
+        (at least 128 workgroups per launch from four 128-token sequences)."""
+        return B is not None and B * S < self.split_rows
 
-    def folded(self, S: int) -> bool:
+    def fused_attention(self, S: int, B: int | None = None) -> bool:
+        """Whether sequences of S tokens take the fused QKV + attention
+        launch (zk_qkv_attn_f16: S of 64 or 128, head_dim 64; not for a
+        small batch of B)."""
+        return (self.fuse_qkv_attention and S in (64, 128) and self.head_dim == 64
+                and not self.small_batch(B, S))
+
+    def folded(self, S: int, B: int | None = None) -> bool:
         """Whether sequences of S tokens run with the LayerNorms folded into
         the GEMMs. With the INT8 FFN only where the QKV projection and
         attention are one launch: at b32 s128 folding took the INT8-FFN
@@ -155,6 +177,8 @@ class BertEncoder:
         (the residual and statistics epilogue of the 256x192-tile int8
         FFN-down and the LayerNorm-folded 256x256 QKV GEMM cost more than the
         Add+LayerNorm launch they replace)."""
+        if self.small_batch(B, S):
+            return False
         return self.fold_ln and (self.int8 is None or self.fused_attention(S))
 
     # ------------------------------------------------------------ INT8 FFN --
@@ -200,6 +224,12 @@ class BertEncoder:
             "q_h": torch.empty((M, H), dtype=torch.int8, device=d),
             "q_u": torch.empty((M, I), dtype=torch.int8, device=d),
         }
+        # split-K partials of the unfolded GEMMs (zero bytes at large M,
+        # where no product is split)
+        H3 = 3 * H
+        ws = max(int(L.load().zk_gemm_workspace_size(M, n, k, L.ZK_F16))
+                 for n, k in ((H3, H), (H, H), (I, H), (H, I)))
+        self._bufs["ws"] = torch.empty(ws, dtype=torch.uint8, device=d) if ws else None
         if self.fold_ln:
             f32 = torch.float32
             self._bufs.update({
@@ -216,12 +246,16 @@ class BertEncoder:
 
     # ------------------------------------------------------------- forward --
     def _gemm(self, a, w, b, out, epi, residual=None, stream=None):
+        """out = epi(a . w^T + b); small-M products split along K through
+        the buffers' workspace (zk_gemm_f16_ws), a fixed-order reduction."""
         M, K = a.shape
         N = w.shape[0]
-        L.call("zk_gemm_f16", a.data_ptr(), w.data_ptr(), out.data_ptr(), M, N, K,
+        ws = self._bufs.get("ws") if self._bufs is not None else None
+        L.call("zk_gemm_f16_ws", a.data_ptr(), w.data_ptr(), out.data_ptr(), M, N, K,
                a.stride(0), w.stride(0), out.stride(0), 1, L.ZK_F16, b.data_ptr(),
                None if residual is None else residual.data_ptr(),
-               0 if residual is None else residual.stride(0), epi, stream)
+               0 if residual is None else residual.stride(0), epi,
+               None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), stream)
 
     def _layer(self, i: int, x: torch.Tensor, out: torch.Tensor, lens, B: int, S: int, stream):
         w = self.layers[i]
@@ -230,7 +264,7 @@ class BertEncoder:
         M = B * S
         qkv, ctx, t, h1, u = bf["qkv"], bf["ctx"], bf["t"], bf["h1"], bf["u"]
         scale = float(1.0 / np.sqrt(D))
-        if self.fused_attention(S):
+        if self.fused_attention(S, B):
             L.call("zk_qkv_attn_f16", x.data_ptr(), w["Wqkv"].data_ptr(), w["bqkv"].data_ptr(),
                    ctx.data_ptr(), B, S, H, nh, None if lens is None else lens.data_ptr(),
                    scale, stream)
@@ -265,7 +299,7 @@ class BertEncoder:
         bf = self._bufs
         stream = torch.cuda.current_stream(self.device).cuda_stream
         stop = len(self.layers) if stop is None else stop
-        if self.folded(S):
+        if self.folded(S, B):
             return self._run_folded(x2, lens, B, S, out, start, stop, stream)
         cur = x2
         for i in range(start, stop):
@@ -299,7 +333,7 @@ class BertEncoder:
             prev = None if first else self.layers[i - 1]
             h2, p2 = (bf["ping"], bf["p2a"]) if i % 2 == 0 else (bf["pong"], bf["p2b"])
             # 1-2. QKV projection (+ LN2 of the previous layer) and attention
-            if self.fused_attention(S):
+            if self.fused_attention(S, B):
                 if first:
                     L.call("zk_qkv_attn_f16", cur.data_ptr(), w["Wqkv"].data_ptr(),
                            w["bqkv"].data_ptr(), ctx.data_ptr(), B, S, H, nh, lp, scale, stream)
@@ -420,12 +454,12 @@ class BertEncoder:
             raise RuntimeError("run forward_layers with the INT8 FFN first")
         B, S = self._bufs["key"]
         bf = self._bufs
-        if self.folded(S):
+        if self.folded(S, B):
             out = bf["ping"] if layer % 2 == 0 else bf["pong"]
         else:
             out = bf["t"]
         return {"h1": bf["h1"], "q_h": bf["q_h"], "q_u": bf["q_u"], "ffn_out": out,
-                "residual": self.folded(S)}
+                "residual": self.folded(S, B)}
 
     # --------------------------------------------------------- HIP graph ----
     def capture(self, B: int, S: int, with_lengths: bool = True):
