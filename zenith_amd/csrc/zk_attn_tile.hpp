@@ -73,16 +73,29 @@ __device__ __forceinline__ void attn32_qk(const f16 *__restrict__ Kt, const f16x
                                           int lane, f32x16 (&s)[2]) {
   const int h32 = lane >> 5;
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
+  for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
+  // the two key blocks' accumulation chains alternate, so consecutive
+  // MFMAs never wait for each other's result
 #pragma unroll
-    for (int c = 0; c < D / 16; ++c) {
-      const int kch = SWZ ? (2 * c + h32) ^ kv_swz(lane & 31) : 2 * c + h32;
+  for (int c = 0; c < D / 16; ++c) {
+    const int kch = SWZ ? (2 * c + h32) ^ kv_swz(lane & 31) : 2 * c + h32;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
       const f16x8 kf = *(const f16x8 *)(Kt + (kb * 32 + (lane & 31)) * KLD + kch * 8);
       s[kb] = mfma32x32x16(kf, qf[c], s[kb]);
     }
   }
+}
+
+// (a, b) = (x of this lane, x of lane ^ 32) in some order, by one
+// v_permlane32_swap (a VALU op, no LDS round trip as with __shfl_xor).
+__device__ __forceinline__ void half_swap(float x, float &a, float &b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
 }
 
 // Phase 2, attn32_softmax: keys >= L and (MASK) masked keys set to -inf,
@@ -125,7 +138,11 @@ __device__ __forceinline__ void attn32_softmax(f32x16 (&s)[2], int t, int L, flo
 #pragma unroll
     for (int r = 0; r < 16; ++r) tmax = smax(tmax, s[kb][r]);
   // finite unless MASK (without a mask, key t*KT < L is valid)
-  tmax = smax(tmax, __shfl_xor(tmax, 32, 64)) * scale_log2;
+  {
+    float a, b;
+    half_swap(tmax, a, b);
+    tmax = smax(a, b) * scale_log2;
+  }
   // Lazy rescaling: the reference point m (log2 units) only moves when the
   // tile max exceeds it by more than 8, so exp2(s - m) <= 256 always fits
   // fp16 and the accumulator is rescaled on a few tiles only. O / l is
@@ -153,8 +170,11 @@ __device__ __forceinline__ void attn32_softmax(f32x16 (&s)[2], int t, int L, flo
       psum += e;
       pf[kb][r >> 3][r & 7] = (f16)e;
     }
-  psum += __shfl_xor(psum, 32, 64);
-  l += psum;
+  {
+    float a, b;
+    half_swap(psum, a, b);
+    l += a + b;  // the same sum in either order (fp32 addition commutes)
+  }
 }
 
 // Phase 3, attn32_pv: O^T[d][q] += V^T[d][key] . P^T[key][q] from the V
@@ -174,12 +194,14 @@ __device__ __forceinline__ void attn32_pv(const f16 *__restrict__ Vt, const f16x
   const int r0 = 4 * (grp >> 1) + (sl >> 2);
   const int fv = SWZ ? kv_swz(r0) : 0;
   const int vch = 2 * (grp & 1) + ((sl & 3) >> 1), vin = 4 * (sl & 1);
+  // the D / 32 output blocks' accumulation chains alternate (each still
+  // accumulates its key blocks in the same order)
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt)
+  for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int c2 = 0; c2 < 2; ++c2)
 #pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2) {
+      for (int dt = 0; dt < D / 32; ++dt) {
         const f16 *row = Vt + (r0 + kb * 32 + c2 * 16) * KLD;
         const int ch = 4 * dt + vch;
         const f16x4 lo = lds_read_tr16(row + (((ch ^ fv) << 3) + vin));
