@@ -558,10 +558,50 @@ def measure_kernels(torch, dev, names=None):
         traffic = pmc_traffic(name)  # counter-measured HBM bytes per launch, if profiled
         if traffic is not None:
             row["traffic"] = traffic
+        if name in VENDOR_GEMMS:
+            vus = vendor_linear_us(torch, dev, *VENDOR_GEMMS[name], iters)
+            row["vendor"] = {"library": "hipBLASLt (torch.nn.functional.linear, fp16, bias "
+                                        "epilogue)", "us": round(vus, 3),
+                             "speedup_of_ours": round(vus / (t * 1e6), 3)}
         out.append(row)
         del launch
         torch.cuda.empty_cache()
     return out
+
+
+# plain GEMM cases (M, K, N) also timed on the vendor library, for scale
+VENDOR_GEMMS = {
+    "gemm_qkv": (4096, 768, 2304), "gemm_out_proj": (4096, 768, 768),
+    "gemm_ffn_up": (4096, 768, 3072), "gemm_ffn_down": (4096, 3072, 768),
+    "gemm_sq1024": (1024, 1024, 1024), "gemm_sq4096": (4096, 4096, 4096),
+    "gemm_sq8192": (8192, 8192, 8192),
+}
+
+
+def vendor_linear_us(torch, dev, M, K, N, iters):
+    """Mean duration (us) of torch.nn.functional.linear (hipBLASLt on ROCm)
+    on the same fp16 shape, with a bias (the library's fused epilogue; no
+    activation), back-to-back launches bracketed by HIP events on torch's
+    stream after a warm-up."""
+    f16 = torch.float16
+    g = torch.Generator(device=dev).manual_seed(7)
+    a = torch.rand((M, K), device=dev, generator=g).to(f16)
+    w = (torch.rand((N, K), device=dev, generator=g) * 0.05).to(f16)
+    b = torch.zeros(N, device=dev, dtype=f16)
+    for _ in range(5):
+        y = torch.nn.functional.linear(a, w, b)
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            y = torch.nn.functional.linear(a, w, b)
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e3 / iters)
+    del y, a, w, b
+    return best
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.md")
