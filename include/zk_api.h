@@ -382,7 +382,7 @@ int zk_gemm_f16_ws(const void *A, const void *B, void *C, int64_t M, int64_t N,
  * serving loops, hosts that forbid allocation). No counterpart in the
  * reference. Same arguments, checks and results as zk_gemm_f16_ws with a
  * workspace of zk_gemm_workspace_size(M, N, K, ZK_F16) bytes: small-M
- * products are split along K, their fp32 partials kept in a static 4 MiB
+ * products are split along K, their fp32 partials kept in a static 8 MiB
  * device array (one per GPU, held until the process ends; the split plan
  * never needs more, and a larger need is rejected with ZK_ERR_UNSUPPORTED).
  * The first call on each device that splits looks up the array's address on

@@ -180,3 +180,16 @@ def test_gemm_workspace_plan():
     assert lib.zk_gemm_workspace_size(4096, 3072, 768, L.ZK_F16) == 0
     assert lib.zk_gemm_workspace_size(64, 64, 64, L.ZK_F16) == 0  # too few K slices
     assert lib.zk_gemm_workspace_size(0, 768, 768, L.ZK_F32) == 0
+    # fp16 FFN-down of one and of four 128-token sequences: 24 and 96 tiles of
+    # 64 x 64; K = 3072 is 48 slices, deep enough for up to two workgroups per
+    # CU at >= 12 slices each (4 splits at M = 512), shallow products keep at
+    # most one per CU (the out-projection at M = 512: 2 splits)
+    part = lambda M, N: M * N * 4  # noqa: E731
+    assert lib.zk_gemm_workspace_size(128, 768, 3072, L.ZK_F16) == 10 * part(128, 768)
+    assert lib.zk_gemm_workspace_size(512, 768, 3072, L.ZK_F16) == 4 * part(512, 768)
+    assert lib.zk_gemm_workspace_size(512, 768, 768, L.ZK_F16) == 2 * part(512, 768)
+    # the largest plan stays within the allocation-free entry point's 8 MiB
+    worst = max(lib.zk_gemm_workspace_size(M, N, K, dt) for M in (64, 128, 320, 512, 960)
+                for N in (64, 768, 1024, 3072) for K in (768, 3072, 16384)
+                for dt in (L.ZK_F16, L.ZK_F32))
+    assert 0 < worst <= 8 << 20

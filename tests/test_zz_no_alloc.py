@@ -36,14 +36,15 @@ def _gemm_pair(dev, M, K, N, epi, tag):
 
 
 def test_noalloc_matches_workspace_entry_point(dev):
-    cases = [(128, 3072, 768, L.ZK_EPI_BIAS, 10),          # 10 splits, 3.75 MiB of partials
+    cases = [(512, 3072, 768, L.ZK_EPI_BIAS, 50),          # 4 splits, 6 MiB of partials
+             (128, 3072, 768, L.ZK_EPI_BIAS, 10),          # smaller: 10 splits, 3.75 MiB
              (64, 768, 768, L.ZK_EPI_BIAS_GELU_ERF, 20),   # smaller: 6 splits
              (4096, 768, 3072, L.ZK_EPI_BIAS, 30)]         # not split: no scratch used
     for M, K, N, epi, tag in cases:
         need, c_ws, c_na, x, w, b = _gemm_pair(dev, M, K, N, epi, tag)
         print(f"noalloc M={M} K={K} N={N} epi={epi}: partials {need} bytes", flush=True)
         assert (need > 0) == (M < 4096)
-        assert need <= 4 << 20
+        assert need <= 8 << 20
         assert torch.equal(c_na, c_ws), (M, K, N)
         ref = ops.matmul_f64(x, w.T) + b
         if epi == L.ZK_EPI_BIAS_GELU_ERF:

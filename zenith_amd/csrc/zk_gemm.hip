@@ -962,7 +962,9 @@ static int launched(bool ok, const char *who, int epi) {
 // sequence of 128 tokens) are split along K: workgroup (tile, split) runs
 // the 64x64 kernel over its K range and writes the raw fp32 partial tile to
 // a caller-provided workspace; splitk_reduce then sums the partials in split
-// order (deterministic) and applies the epilogue.
+// order (deterministic) and applies the epilogue. Only products of fewer than
+// 128 tiles split, into at most 512 / t64 splits, so the partials (splits x
+// M x N fp32) never exceed 512 x 64 x 64 x 4 bytes = 8 MiB.
 struct SplitPlan {
   int splits;  // 1: no split
   int nk_per;  // 128-byte K slices per split
@@ -977,6 +979,18 @@ static SplitPlan plan_split(int64_t M, int64_t N, int64_t K, int elem) {
   int64_t splits = 256 / t64;
   if (splits > 16) splits = 16;
   if (splits > nk_all / 2) splits = nk_all / 2;
+  // Deep K (>= 24 slices): up to two workgroups per CU, keeping at least 12
+  // slices per split. At M = 512 (four 128-token sequences) FFN-down
+  // (K = 3072) then runs 4 splits instead of 2: the b4 s128 encoder 0.752
+  // -> 0.677 ms per step, b1 and b2 unchanged (their plan is the same).
+  // Letting shallow products (QKV, out-projection, FFN-up) follow the same
+  // rule left them unsplit: b1 0.605 -> 0.628 ms.
+  if (nk_all >= 24) {
+    int64_t deep = 512 / t64;
+    if (deep > 16) deep = 16;
+    if (deep > nk_all / 12) deep = nk_all / 12;
+    if (deep > splits) splits = deep;
+  }
   if (splits < 2) return sp;
   const int64_t per = (nk_all + splits - 1) / splits;
   splits = (nk_all + per - 1) / per;  // no empty split

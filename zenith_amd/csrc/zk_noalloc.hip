@@ -4,9 +4,9 @@
 // in a caller workspace live here in a file-scope device array instead.
 //
 // Size: the split plan only splits products whose 64 x 64 tiles number
-// t64 < 128, into at most 256 / t64 splits, and M * N <= t64 * 64 * 64, so
-// the partials (splits * M * N fp32) never exceed 256 * 4096 * 4 bytes =
-// 4 MiB: the array holds exactly that. Each GPU the library runs on holds its
+// t64 < 128, into at most 512 / t64 splits, and M * N <= t64 * 64 * 64, so
+// the partials (splits * M * N fp32) never exceed 512 * 4096 * 4 bytes =
+// 8 MiB: the array holds exactly that. Each GPU the library runs on holds its
 // own copy until the process ends.
 //
 // The array's host-side name is not a device address: its address on each
@@ -23,7 +23,7 @@
 
 namespace zk {
 
-constexpr int64_t kScratchBytes = 4ll << 20;
+constexpr int64_t kScratchBytes = 8ll << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;
