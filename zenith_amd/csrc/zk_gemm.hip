@@ -1020,6 +1020,35 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ w
   }
 }
 
+// splitk_reduce on four consecutive columns per thread: 16-byte partial
+// loads and one 8- or 16-byte store (N, ldc and ldr multiples of 4, aligned
+// operands). The same sum in the same order as splitk_reduce.
+template <int EPI, typename OutT>
+__global__ __launch_bounds__(256) void splitk_reduce4(const float *__restrict__ ws, int splits,
+                                                      int64_t stride, int M, int N,
+                                                      const OutT *__restrict__ bias,
+                                                      const OutT *__restrict__ res, int64_t ldr,
+                                                      OutT *__restrict__ C, int64_t ldc) {
+  typedef OutT OutT4 __attribute__((ext_vector_type(4)));
+  const int64_t total = (int64_t)M * N / 4;
+  const int64_t step = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += step) {
+    const int64_t e = 4 * i, m = e / N, n = e % N;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < splits; ++sp) v += *(const f32x4 *)(ws + sp * stride + e);
+    OutT4 b4 = {}, r4 = {}, o4;
+    if (EPI != ZK_EPI_NONE) b4 = *(const OutT4 *)(bias + n);
+    if (EPI == ZK_EPI_BIAS_RESIDUAL) r4 = *(const OutT4 *)(res + m * ldr + n);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float t = epilogue<EPI>(v[k], EPI != ZK_EPI_NONE ? to_f(b4[k]) : 0.f);
+      if (EPI == ZK_EPI_BIAS_RESIDUAL) t += to_f(r4[k]);
+      o4[k] = (OutT)t;
+    }
+    *(OutT4 *)(C + m * ldc + n) = o4;
+  }
+}
+
 // p describes the final product (C, ldc, bias, residual); the partials go to
 // ws (at least split_ws_bytes). OP is F16Op or F32Op.
 // Returns whether both kernels were launched (false for an epilogue the
@@ -1041,13 +1070,27 @@ template <class OP, typename OutT>
   q.nk_per = sp.nk_per;
   q.split_stride = (int64_t)p.M * p.N;
   if (!launch_mfma<OP, float, false>(q, ZK_EPI_NONE, s, 3)) return false;
-  const int64_t total = (int64_t)p.M * p.N;
-  int64_t g = (total + 255) / 256;
-  if (g > 4096) g = 4096;
   const OutT *bias = (const OutT *)p.bias, *res = (const OutT *)p.res;
   OutT *C = (OutT *)p.C;
-#define ZK_R(E) splitk_reduce<E, OutT><<<(unsigned)g, 256, 0, s>>>( \
-    ws, sp.splits, q.split_stride, p.M, p.N, bias, res, p.ldr, C, p.ldc)
+  // four columns per thread when every row starts on a 4-element boundary
+  constexpr int64_t VB = 4 * sizeof(OutT);  // bytes of four outputs
+  const bool vec = p.N % 4 == 0 && p.ldc % 4 == 0 && aligned16(ws) && (uintptr_t)C % VB == 0 &&
+                   (!bias || (uintptr_t)bias % VB == 0) &&
+                   (epi != ZK_EPI_BIAS_RESIDUAL || (p.ldr % 4 == 0 && (uintptr_t)res % VB == 0));
+  const int64_t total = (int64_t)p.M * p.N / (vec ? 4 : 1);
+  int64_t g = (total + 255) / 256;
+  if (g > 4096) g = 4096;
+#define ZK_R(E)                                                                              \
+  do {                                                                                       \
+    if (vec)                                                                                 \
+      splitk_reduce4<E, OutT><<<(unsigned)g, 256, 0, s>>>(ws, sp.splits, q.split_stride,   \
+                                                          p.M, p.N, bias, res, p.ldr, C,   \
+                                                          p.ldc);                          \
+    else                                                                                     \
+      splitk_reduce<E, OutT><<<(unsigned)g, 256, 0, s>>>(ws, sp.splits, q.split_stride,    \
+                                                         p.M, p.N, bias, res, p.ldr, C,    \
+                                                         p.ldc);                           \
+  } while (0)
   switch (epi) {
     case ZK_EPI_NONE: ZK_R(ZK_EPI_NONE); break;
     case ZK_EPI_BIAS: ZK_R(ZK_EPI_BIAS); break;
