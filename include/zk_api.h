@@ -377,6 +377,27 @@ int zk_gemm_f16_ws(const void *A, const void *B, void *C, int64_t M, int64_t N,
                    int out_dtype, const void *bias, const void *residual, int64_t ldr,
                    int epilogue, void *workspace, int64_t ws_bytes, void *stream);
 
+/* Linear + residual + LayerNorm (the post-LN block closing a BERT attention
+ * or FFN half), fp16:
+ *   T = fp16(A[M,K] . W[N,K]^T + bias),  Y = LayerNorm(T + R) * gamma + beta
+ * bit-identical to zk_gemm_f16_ws (ZK_EPI_BIAS, fp16 out, ldc = N) into T
+ * followed by zk_layernorm(T, R). When the product splits along K (a
+ * workspace of at least zk_gemm_workspace_size(M, N, K, ZK_F16) bytes, as
+ * for zk_gemm_f16_ws) into at most M / 32 splits, and N is a multiple of 8
+ * up to 8192 with 16-byte aligned bias, R, gamma, beta and Y, the split
+ * partials are read straight by the LayerNorm launch, which forms the rows
+ * of T itself: one launch fewer, and T is not written. Otherwise T ([M, N]
+ * fp16, contiguous) holds the product as the pair would leave it. R, Y: [M, N] contiguous; bias,
+ * gamma, beta: [N]. Operand rules of zk_gemm_f16 (W as [N, K], K, lda, ldw
+ * multiples of 8, A and W 16-byte aligned). No single reference
+ * counterpart: the out-projection / FFN-down linear and the Add+LayerNorm
+ * after it (benchmarks/bert_fp16_full.py:128-143; fused_add_layernorm
+ * core/src/fused_kernels.cu:145-221). */
+int zk_gemm_f16_add_ln(const void *A, const void *W, const void *bias, const void *R,
+                       const void *gamma, const void *beta, void *T, void *Y, int64_t M,
+                       int64_t N, int64_t K, int64_t lda, int64_t ldw, float eps,
+                       void *workspace, int64_t ws_bytes, void *stream);
+
 /* zk_gemm_f16 that allocates nothing and takes no workspace: for callers
  * that cannot allocate device memory (code under HIP-graph capture, tight
  * serving loops, hosts that forbid allocation). No counterpart in the

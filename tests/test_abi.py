@@ -136,6 +136,18 @@ def test_library_exports_every_declared_symbol():
      L.ZK_ERR_INVALID),  # unknown epilogue
     (lambda lib: lib.zk_linear_f32(16, 16, 16, 8, 8, 8, 4, 8, 8, None, None, 0, 0, None, 0, None),
      L.ZK_ERR_INVALID),  # ldx < K
+    (lambda lib: lib.zk_gemm_f16_add_ln(16, 16, 16, 16, 16, 16, None, 16, 8, 8, 8, 8, 8, 1e-12,
+                                        None, 0, None), L.ZK_ERR_INVALID),  # no product buffer
+    (lambda lib: lib.zk_gemm_f16_add_ln(16, 16, None, 16, 16, 16, 16, 16, 8, 8, 8, 8, 8, 1e-12,
+                                        None, 0, None), L.ZK_ERR_INVALID),  # no bias
+    (lambda lib: lib.zk_gemm_f16_add_ln(16, 16, 16, 16, 16, 16, 16, 16, 8, 8, 8, 8, 8, -1.0,
+                                        None, 0, None), L.ZK_ERR_INVALID),  # eps
+    (lambda lib: lib.zk_gemm_f16_add_ln(16, 16, 16, 16, 16, 16, 16, 16, 8, 8, 8, 4, 8, 1e-12,
+                                        None, 0, None), L.ZK_ERR_INVALID),  # lda < K
+    (lambda lib: lib.zk_gemm_f16_add_ln(16, 16, 16, 16, 16, 16, 16, 16, 8, 8, 12, 12, 12, 1e-12,
+                                        None, 0, None), L.ZK_ERR_UNSUPPORTED),  # K % 8
+    (lambda lib: lib.zk_gemm_f16_add_ln(16, 16, 16, 16, 16, 16, 16, 16, 8, 8, 8, 8, 8, 1e-12,
+                                        None, -1, None), L.ZK_ERR_INVALID),  # workspace size
 ])
 def test_argument_errors(call, code):
     lib = L.load()

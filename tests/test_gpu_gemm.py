@@ -291,3 +291,60 @@ def test_linear_f32_c_abi(dev, M, K, N, epi):
     elif epi == "residual":
         ref = ref + r
     np.testing.assert_allclose(y.cpu().numpy(), ref, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("M,K,N,pad", [(128, 3072, 768, 192), (512, 3072, 768, 192),
+                                       (128, 768, 768, 0), (512, 768, 768, 0),
+                                       (256, 3072, 768, 192), (4096, 768, 768, 0),
+                                       (96, 1000, 200, 24), (37, 3072, 96, 0),
+                                       (320, 1024, 64, 8)])
+def test_gemm_add_layernorm(dev, M, K, N, pad):
+    """zk_gemm_f16_add_ln = the pair it replaces, bit for bit: zk_gemm_f16_ws
+    (bias epilogue, fp16 out) into T, then zk_layernorm(T, R). Products that
+    split along K into at most M / 32 splits take the fused path (the
+    LayerNorm launch sums the split partials itself), the others the pair;
+    both against the float64 product
+    and the oracle's Add+LayerNorm at the fp16 bar. A and W with padded rows
+    (the encoder's FFN intermediate), K not a multiple of the 128-byte slice
+    (1000), N a multiple of 8 only (200, 96) and a ragged M (37)."""
+    from zenith_amd import _lib as L
+
+    lib = L.load()
+    x = synthetic.round_f16(synthetic.normal((M, K), tag=60))
+    w = synthetic.round_f16(synthetic.normal((N, K), tag=61, std=0.03))
+    b = synthetic.round_f16(synthetic.normal((N,), tag=62, std=0.5))
+    r = synthetic.round_f16(synthetic.normal((M, N), tag=63))
+    g = synthetic.round_f16(1 + synthetic.normal((N,), tag=64, std=0.1))
+    be = synthetic.round_f16(synthetic.normal((N,), tag=65, std=0.1))
+    tx = torch.zeros((M, K + pad), dtype=torch.float16, device=dev)
+    tx[:, :K] = _t(x, dev, torch.float16)
+    tw = torch.zeros((N, K + pad), dtype=torch.float16, device=dev)
+    tw[:, :K] = _t(w, dev, torch.float16)
+    tb, tr, tg, tbe = (_t(a, dev, torch.float16) for a in (b, r, g, be))
+    need = int(lib.zk_gemm_workspace_size(M, N, K, L.ZK_F16))
+    ws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    t_pair = torch.empty((M, N), dtype=torch.float16, device=dev)
+    y_pair = torch.empty((M, N), dtype=torch.float16, device=dev)
+    L.call("zk_gemm_f16_ws", tx.data_ptr(), tw.data_ptr(), t_pair.data_ptr(), M, N, K,
+           tx.stride(0), tw.stride(0), N, 1, L.ZK_F16, tb.data_ptr(), None, 0, L.ZK_EPI_BIAS,
+           ws.data_ptr(), need, s)
+    L.call("zk_layernorm", t_pair.data_ptr(), tr.data_ptr(), tg.data_ptr(), tbe.data_ptr(),
+           y_pair.data_ptr(), M, N, 1e-12, L.ZK_F16, s)
+    t_buf = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+    y = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+    L.call("zk_gemm_f16_add_ln", tx.data_ptr(), tw.data_ptr(), tb.data_ptr(), tr.data_ptr(),
+           tg.data_ptr(), tbe.data_ptr(), t_buf.data_ptr(), y.data_ptr(), M, N, K, tx.stride(0),
+           tw.stride(0), 1e-12, ws.data_ptr(), need, s)
+    torch.cuda.synchronize()
+    # split products of at least 32 rows per split read the partials in the LayerNorm launch
+    fused = need > 0 and need // (M * N * 4) * 32 <= M
+    assert torch.equal(y, y_pair), (M, K, N)
+    if not fused:
+        assert torch.equal(t_buf, t_pair)
+    t_ref = synthetic.round_f16(ops.matmul_f64(x, w.T).astype(np.float32) + b)  # T is fp16
+    ref = ops.add_layernorm(t_ref, r, g, be, 1e-12)
+    ok, worst = fp16_tol(y.float().cpu().numpy(), ref)
+    assert ok, worst
+    print(f"gemm+add+LN M={M} K={K} N={N}: {'fused over split partials' if fused else 'pair'}, "
+          f"bit-identical to the pair", flush=True)

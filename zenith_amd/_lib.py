@@ -76,6 +76,8 @@ SIGNATURES: dict[str, list] = {
     "zk_gemm_workspace_size": [_i64, _i64, _i64, _i32],
     "zk_gemm_f16_ws": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
                        _vp, _vp, _i64, _i32, _vp, _i64, _vp],
+    "zk_gemm_f16_add_ln": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                           _f32, _vp, _i64, _vp],
     "zk_gemm_f32_ws": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _vp, _i64, _vp],
     "zk_gemm_f16_noalloc": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
                             _vp, _vp, _i64, _i32, _vp],

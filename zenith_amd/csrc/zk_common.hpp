@@ -54,6 +54,18 @@ int gemm_f16_impl(const void *A, const void *B, void *C, int64_t M, int64_t N, i
                   const void *bias, const void *residual, int64_t ldr, int epilogue, void *ws,
                   int64_t ws_bytes, void *stream);
 
+// Add+LayerNorm over split-K partials (zk_layernorm.hip): y = LN(x + res)
+// with x = fp16(sum of the `splits` fp32 partials [rows][hidden], split s at
+// ws + s * stride, + bias), the same values and the same LayerNorm as
+// splitk_reduce (ZK_EPI_BIAS) followed by zk_layernorm. ln_partials_ok says
+// whether the shape and alignments allow it (hidden a multiple of 8 up to
+// 8192, 16-byte aligned operands).
+bool ln_partials_ok(const float *ws, int64_t stride, const void *bias, const void *res,
+                    const void *g, const void *b, const void *y, int64_t rows, int64_t hidden);
+int ln_add_partials_f16(const float *ws, int splits, int64_t stride, const void *bias,
+                        const void *res, const void *g, const void *b, void *y, int64_t rows,
+                        int64_t hidden, float eps, hipStream_t s);
+
 // Symmetric int8 quantisation of one value,
 //   q = clamp(round_half_even(RN(x / scale)), -128, 127)
 // (quantize_f32_to_int8_kernel, core/src/cuda_kernels.cu:926-927), with

@@ -1244,6 +1244,56 @@ extern "C" int zk_gemm_f16_ws(const void *A, const void *B, void *C, int64_t M, 
                        epilogue, workspace, ws_bytes, stream);
 }
 
+// Linear + residual + LayerNorm. A product that splits along K (and whose
+// rows the wave LayerNorm can hold) runs as its split partials plus one
+// LayerNorm launch that forms the rows from the partials; anything else as
+// zk_gemm_f16_ws into T followed by zk_layernorm. Both give the pair's
+// result bit for bit. The LayerNorm launch has one wavefront per row, each
+// reading its row's partials of every split: that pays while there are at
+// least 32 rows per split. BERT encoder per step (12 layers, s128), pair ->
+// partials read by the LayerNorm: b2 (out-projection and FFN-down in 5
+// splits) 0.635 -> 0.617 ms, b4 (2 and 4 splits) 0.675 -> 0.643 ms; at b1
+// (6 and 10 splits of 128 rows) it was 0.604 -> 0.621 ms, so b1 keeps the
+// pair, whose reduction spreads over many more workgroups.
+extern "C" int zk_gemm_f16_add_ln(const void *A, const void *W, const void *bias, const void *R,
+                                  const void *gamma, const void *beta, void *T, void *Y,
+                                  int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw,
+                                  float eps, void *workspace, int64_t ws_bytes, void *stream) {
+  const char *who = "zk_gemm_f16_add_ln";
+  int st = check_dims(who, M, N, K);
+  if (st) return st;
+  if (M == 0 || N == 0) return ZK_OK;
+  if (!A || !W || !bias || !R || !gamma || !beta || !T || !Y)
+    return fail(ZK_ERR_INVALID, "%s: null pointer", who);
+  if (!(eps >= 0.0f)) return fail(ZK_ERR_INVALID, "%s: eps must be >= 0", who);
+  if (ws_bytes < 0) return fail(ZK_ERR_INVALID, "%s: negative workspace size", who);
+  if (lda < K || ldw < K) return fail(ZK_ERR_INVALID, "%s: leading dimension too small", who);
+  if (K == 0) return fail(ZK_ERR_UNSUPPORTED, "%s: K == 0", who);
+  if (K % 8 || lda % 8 || ldw % 8 || !aligned16(A) || !aligned16(W))
+    return fail(ZK_ERR_UNSUPPORTED,
+                "%s: K, lda, ldw must be multiples of 8 and A, W 16-byte aligned", who);
+  if ((st = check_span(who, lda, ldw, K, 2))) return st;
+  hipStream_t s = as_stream(stream);
+  const SplitPlan sp = plan_split(M, N, K, 2);
+  const float *ws = (const float *)workspace;
+  if (ws && sp.splits > 1 && ws_bytes >= split_ws_bytes(M, N, sp) && sp.splits * 32 <= M &&
+      ln_partials_ok(ws, M * N, bias, R, gamma, beta, Y, M, N)) {
+    GemmParams q{A, W, workspace, (int)M, (int)N, (int)K, lda, ldw, N, nullptr, nullptr, 0, 1.f,
+                 nullptr, 0};
+    q.splits = sp.splits;
+    q.nk_per = sp.nk_per;
+    q.split_stride = M * N;
+    if (!launch_mfma<F16Op, float, false>(q, ZK_EPI_NONE, s, 3))
+      return fail(ZK_ERR_UNSUPPORTED, "%s: no partial-product kernel for this shape", who);
+    if ((st = check_launch(who))) return st;
+    return ln_add_partials_f16(ws, sp.splits, M * N, bias, R, gamma, beta, Y, M, N, eps, s);
+  }
+  st = gemm_f16_impl(A, W, T, M, N, K, lda, ldw, N, 1, ZK_F16, bias, nullptr, 0, ZK_EPI_BIAS,
+                     workspace, ws_bytes, stream);
+  if (st) return st;
+  return zk_layernorm(T, R, gamma, beta, Y, M, N, eps, ZK_F16, stream);
+}
+
 // Fused QKV projection + attention (sequences of 64 or 128 tokens, head dim
 // 64): one 256 x 192 tile per workgroup, the q, k and v columns of one head
 // for 256 rows, with the attention of the tile's sequences in its epilogue.

@@ -8,6 +8,8 @@
 // butterflies. Rows whose hidden size is not a multiple of the vector width
 // (or larger than the register budget) take a block-per-row kernel that
 // re-reads the row from cache.
+#include <type_traits>
+
 #include "zk_common.hpp"
 
 namespace zk {
@@ -31,15 +33,27 @@ template <typename T> struct ResLn {
   const T *g, *b;    // [hidden]
 };
 
+// PART: the input rows are not read from x but formed from the fp32 split-K
+// partials of a GEMM, [splits][rows][hidden] (split s at ws + s * stride),
+// summed in split order from zero, plus the bias, rounded to T: exactly the
+// values splitk_reduce (epilogue ZK_EPI_BIAS) would store for x.
+template <typename T> struct PartIn {
+  const float *ws;
+  int splits;
+  int64_t stride;
+  const T *bias;  // [hidden]
+};
+
 // LPR lanes per row (64 / LPR rows per wavefront): a 768-wide fp16 row is 96
 // 16-byte vectors, so two rows per wavefront give every lane exactly three.
 // Q8: also write q = quant(y) as int8 (the fp16 output value quantised with
 // scale qs), for an int8 GEMM that consumes the normalised rows.
-template <typename T, int MAXV, int RES, int LPR, bool Q8>
+template <typename T, int MAXV, int RES, int LPR, bool Q8, bool PART = false>
 __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
     const T *__restrict__ x, const T *__restrict__ res,
     const T *__restrict__ gamma, const T *__restrict__ beta, T *__restrict__ y,
-    int8_t *__restrict__ q, float qs, int64_t rows, int hidden, float eps, ResLn<T> rl) {
+    int8_t *__restrict__ q, float qs, int64_t rows, int hidden, float eps, ResLn<T> rl,
+    PartIn<T> pin) {
   constexpr bool PRE = RES == kResPre || RES == kResPreLn;
   typedef typename LnVec<T>::type V;
   constexpr int W = LnVec<T>::n;
@@ -62,7 +76,26 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
   for (int k = 0; k < MAXV; ++k) {
     const int idx = sub + k * LPR;
     if (live && idx < nvec) {
-      V a = xr[idx];
+      V a;
+      if constexpr (PART) {
+        static_assert(W == 8, "partials are summed 8 columns at a time");
+        const float *pp = pin.ws + (row * hidden + (int64_t)idx * W);
+        float t[W] = {};
+        for (int sp = 0; sp < pin.splits; ++sp) {
+          const f32x4 lo = *(const f32x4 *)(pp + sp * pin.stride);
+          const f32x4 hi = *(const f32x4 *)(pp + sp * pin.stride + 4);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            t[j] += lo[j];
+            t[j + 4] += hi[j];
+          }
+        }
+        const V bv = reinterpret_cast<const V *>(pin.bias)[idx];
+#pragma unroll
+        for (int j = 0; j < W; ++j) a[j] = (T)(t[j] + (float)bv[j]);
+      } else {
+        a = xr[idx];
+      }
       V r, rg, rb;
       if (PRE) r = rr[idx];
       if (RES == kResPreLn) {
@@ -195,7 +228,8 @@ static void ln_wave_launch(const T *x, const T *r, const T *g, const T *b, T *y,
   const unsigned grid = (unsigned)((rows + rows_per_block - 1) / rows_per_block);
 #define ZK_LNW(RES, QQ) \
   ln_wave_kernel<T, MAXV, RES, LPR, QQ><<<grid, kLnWaves * kWave, 0, s>>>(x, r, g, b, y, q, qs, \
-                                                                         rows, hidden, eps, rl)
+                                                                         rows, hidden, eps, rl, \
+                                                                         PartIn<T>{})
   if (r && post) {
     if constexpr (!Q8) ZK_LNW(kResPost, false);
   } else if (r && rl.ms) {
@@ -206,6 +240,27 @@ static void ln_wave_launch(const T *x, const T *r, const T *g, const T *b, T *y,
     ZK_LNW(kResNone, Q8);
   }
 #undef ZK_LNW
+}
+
+// (vectors per lane MAXV, lanes per row LPR) of the wave kernel for `rows`
+// rows of `nvec` vectors (nvec <= 16 * 64): every launch of a given shape,
+// from rows or from split-K partials, takes its shape from here and so sums
+// in one order. With few rows (under 2048: a few sequences) a whole
+// wavefront per row gives four rows per workgroup instead of eight, twice
+// the workgroups.
+template <class F>
+static void ln_pick(int64_t rows, int64_t nvec, F &&launch) {
+  using std::integral_constant;
+  const bool few = rows < 2048;
+  if (few && nvec <= 64) launch(integral_constant<int, 1>(), integral_constant<int, 64>());
+  else if (few && nvec <= 128) launch(integral_constant<int, 2>(), integral_constant<int, 64>());
+  else if (nvec <= 32) launch(integral_constant<int, 1>(), integral_constant<int, 32>());
+  else if (nvec <= 64) launch(integral_constant<int, 2>(), integral_constant<int, 32>());
+  else if (nvec <= 96) launch(integral_constant<int, 3>(), integral_constant<int, 32>());
+  else if (nvec <= 128) launch(integral_constant<int, 4>(), integral_constant<int, 32>());
+  else if (nvec <= 256) launch(integral_constant<int, 4>(), integral_constant<int, 64>());
+  else if (nvec <= 512) launch(integral_constant<int, 8>(), integral_constant<int, 64>());
+  else launch(integral_constant<int, 16>(), integral_constant<int, 64>());
 }
 
 // post: the residual is added after normalisation (LN(x) + r) instead of
@@ -228,21 +283,10 @@ static int ln_impl(const void *xv, const void *rv, const void *gv,
     const int h = (int)hidden;
     // 32 lanes per row while a row fits in 4 vectors per lane (H <= 1024 in
     // fp16), else a whole wavefront per row.
-#define ZK_LN(MV, LPR) \
-  ln_wave_launch<T, MV, LPR, Q8>(x, r, g, b, y, q, qs, rows, h, eps, post, rl, s)
-    // With few rows (under 2048: a few sequences) a whole wavefront per row
-    // gives four rows per workgroup instead of eight, twice the workgroups.
-    const bool few = rows < 2048;
-    if (few && nvec <= 64) ZK_LN(1, 64);
-    else if (few && nvec <= 128) ZK_LN(2, 64);
-    else if (nvec <= 32) ZK_LN(1, 32);
-    else if (nvec <= 64) ZK_LN(2, 32);
-    else if (nvec <= 96) ZK_LN(3, 32);
-    else if (nvec <= 128) ZK_LN(4, 32);
-    else if (nvec <= 256) ZK_LN(4, 64);
-    else if (nvec <= 512) ZK_LN(8, 64);
-    else ZK_LN(16, 64);
-#undef ZK_LN
+    ln_pick(rows, nvec, [&](auto mv, auto lpr) {
+      ln_wave_launch<T, decltype(mv)::value, decltype(lpr)::value, Q8>(x, r, g, b, y, q, qs, rows,
+                                                                      h, eps, post, rl, s);
+    });
   } else {
     if (rows > 0x7fffffff)
       return fail(ZK_ERR_UNSUPPORTED, "zk_layernorm: too many rows for the generic path");
@@ -260,6 +304,29 @@ static int ln_impl(const void *xv, const void *rv, const void *gv,
 #undef ZK_LNB
   }
   return check_launch("zk_layernorm");
+}
+
+bool ln_partials_ok(const float *ws, int64_t stride, const void *bias, const void *res,
+                    const void *g, const void *b, const void *y, int64_t rows, int64_t hidden) {
+  return hidden > 0 && hidden % 8 == 0 && hidden / 8 <= 16 * kWave && stride % 4 == 0 &&
+         (rows + kLnWaves - 1) / kLnWaves <= 0x7fffffff && aligned16(ws) && aligned16(bias) &&
+         aligned16(res) && aligned16(g) && aligned16(b) && aligned16(y);
+}
+
+int ln_add_partials_f16(const float *ws, int splits, int64_t stride, const void *bias,
+                        const void *res, const void *g, const void *b, void *y, int64_t rows,
+                        int64_t hidden, float eps, hipStream_t s) {
+  const PartIn<f16> pin{ws, splits, stride, (const f16 *)bias};
+  const int h = (int)hidden;
+  ln_pick(rows, hidden / 8, [&](auto mv, auto lpr) {
+    constexpr int MV = decltype(mv)::value, LPR = decltype(lpr)::value;
+    constexpr int rows_per_block = kLnWaves * (kWave / LPR);
+    const unsigned grid = (unsigned)((rows + rows_per_block - 1) / rows_per_block);
+    ln_wave_kernel<f16, MV, kResPre, LPR, false, true><<<grid, kLnWaves * kWave, 0, s>>>(
+        nullptr, (const f16 *)res, (const f16 *)g, (const f16 *)b, (f16 *)y, nullptr, 1.f, rows,
+        h, eps, ResLn<f16>{nullptr, nullptr, nullptr}, pin);
+  });
+  return check_launch("zk_gemm_f16_add_ln");
 }
 
 }  // namespace zk

@@ -273,6 +273,18 @@ class BertEncoder:
                0 if residual is None else residual.stride(0), epi,
                None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), stream)
 
+    def _gemm_add_ln(self, a, w, b, res, g, beta, tmp, out, stream):
+        """out = LayerNorm(a . w^T + b + res) (zk_gemm_f16_add_ln): where the
+        product splits along K, the LayerNorm launch sums the split partials
+        itself (one launch fewer); otherwise the product goes through tmp."""
+        M, K = a.shape
+        N = w.shape[0]
+        ws = self._bufs.get("ws") if self._bufs is not None else None
+        L.call("zk_gemm_f16_add_ln", a.data_ptr(), w.data_ptr(), b.data_ptr(), res.data_ptr(),
+               g.data_ptr(), beta.data_ptr(), tmp.data_ptr(), out.data_ptr(), M, N, K,
+               a.stride(0), w.stride(0), self.eps, None if ws is None else ws.data_ptr(),
+               0 if ws is None else ws.numel(), stream)
+
     def _layer(self, i: int, x: torch.Tensor, out: torch.Tensor, lens, B: int, S: int, stream):
         w = self.layers[i]
         bf = self._bufs
@@ -287,26 +299,26 @@ class BertEncoder:
         else:
             self._gemm(x, w["Wqkv"], w["bqkv"], qkv, L.ZK_EPI_BIAS, stream=stream)
             self._attention(qkv, ctx, lens, B, S, stream)
-        self._gemm(ctx, w["Wo"], w["bo"], t, L.ZK_EPI_BIAS, stream=stream)
         if self.int8 is None:
-            L.call("zk_layernorm", t.data_ptr(), x.data_ptr(), w["ln1_g"].data_ptr(),
-                   w["ln1_b"].data_ptr(), h1.data_ptr(), M, H, self.eps, L.ZK_F16, stream)
+            # out-projection + Add+LN1, FFN-up + GELU, FFN-down + Add+LN2
+            self._gemm_add_ln(ctx, w["Wo"], w["bo"], x, w["ln1_g"], w["ln1_b"], t, h1, stream)
             self._gemm(h1, w["Wi"], w["bi"], u, self.gelu_epi, stream=stream)
-            self._gemm(u, w["Wo2"], w["bo2"], t, L.ZK_EPI_BIAS, stream=stream)
-        else:
-            # Add+LN1 also writes the int8 FFN input; FFN-up re-quantises its
-            # GELU output in the epilogue (no fp16 intermediate).
-            q = self.int8[i]
-            qh, qu = bf["q_h"], bf["q_u"]
-            L.call("zk_layernorm_q8", t.data_ptr(), x.data_ptr(), w["ln1_g"].data_ptr(),
-                   w["ln1_b"].data_ptr(), h1.data_ptr(), qh.data_ptr(), M, H, self.eps,
-                   q["s_x"], stream)
-            L.call("zk_gemm_i8_requant", qh.data_ptr(), q["Wi_q"].data_ptr(), qu.data_ptr(), M,
-                   self.ffn, H, H, H, qu.stride(0), q["s_x"], q["s_wi"].data_ptr(),
-                   w["bi"].data_ptr(), self.gelu_epi, q["s_h"], stream)
-            L.call("zk_gemm_i8", qu.data_ptr(), q["Wo2_q"].data_ptr(), t.data_ptr(), M, H, self.ffn,
-                   qu.stride(0), q["Wo2_q"].stride(0), H, q["s_h"], q["s_wo2"].data_ptr(),
-                   w["bo2"].data_ptr(), None, 0, L.ZK_EPI_BIAS, L.ZK_F16, stream)
+            self._gemm_add_ln(u, w["Wo2"], w["bo2"], h1, w["ln2_g"], w["ln2_b"], t, out, stream)
+            return
+        # INT8 FFN: Add+LN1 also writes the int8 FFN input; FFN-up re-quantises
+        # its GELU output in the epilogue (no fp16 intermediate).
+        self._gemm(ctx, w["Wo"], w["bo"], t, L.ZK_EPI_BIAS, stream=stream)
+        q = self.int8[i]
+        qh, qu = bf["q_h"], bf["q_u"]
+        L.call("zk_layernorm_q8", t.data_ptr(), x.data_ptr(), w["ln1_g"].data_ptr(),
+               w["ln1_b"].data_ptr(), h1.data_ptr(), qh.data_ptr(), M, H, self.eps,
+               q["s_x"], stream)
+        L.call("zk_gemm_i8_requant", qh.data_ptr(), q["Wi_q"].data_ptr(), qu.data_ptr(), M,
+               self.ffn, H, H, H, qu.stride(0), q["s_x"], q["s_wi"].data_ptr(),
+               w["bi"].data_ptr(), self.gelu_epi, q["s_h"], stream)
+        L.call("zk_gemm_i8", qu.data_ptr(), q["Wo2_q"].data_ptr(), t.data_ptr(), M, H, self.ffn,
+               qu.stride(0), q["Wo2_q"].stride(0), H, q["s_h"], q["s_wo2"].data_ptr(),
+               w["bo2"].data_ptr(), None, 0, L.ZK_EPI_BIAS, L.ZK_F16, stream)
         L.call("zk_layernorm", t.data_ptr(), h1.data_ptr(), w["ln2_g"].data_ptr(),
                w["ln2_b"].data_ptr(), out.data_ptr(), M, H, self.eps, L.ZK_F16, stream)
 
