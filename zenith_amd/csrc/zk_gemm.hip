@@ -336,6 +336,32 @@ void gemm_mfma_kernel(GemmParams p) {
     for (int q = 0; q < kLnMaxParts; ++q)
       ln_pr[q] = mine && q < p.ln_nparts ? src[q] : make_float2(0.f, 0.f);
   }
+  // The epilogue's per-column constants of this lane's TN columns: bias,
+  // dequantisation scale, or the folded LayerNorm's column sums and offsets
+  // (col_s: scale, col_c: offset). Loaded here with the row statistics, so
+  // that their latency passes under the main loop instead of after the last
+  // MFMA.
+  constexpr bool LN_COLS = EPI == kEpiLnIn || EPI == kEpiLnInGelu;
+  typedef typename std::conditional<std::is_same<OutT, int8_t>::value, f16, OutT>::type BiasT;
+  float col_s[TN], col_c[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int col = n0 + wn * WTN + j * MS + lane % MS;
+    col_s[j] = 1.f;
+    col_c[j] = 0.f;
+    if constexpr (EPI == kEpiQkvAttn) {  // N is a whole number of 192-column tiles
+      const bool ln = p.ln_part != nullptr;
+      col_s[j] = ln ? p.ln_s[col] : 0.f;
+      col_c[j] = ln ? p.ln_c[col] : to_f(((const f16 *)p.bias)[col]);
+    } else if (col < p.N) {
+      if (EPI != ZK_EPI_NONE && !LN_COLS) col_c[j] = to_f(((const BiasT *)p.bias)[col]);
+      if (DEQ) col_s[j] = p.s_x * p.s_w[col];
+      if (LN_COLS) {
+        col_s[j] = p.ln_s[col];
+        col_c[j] = p.ln_c[col];
+      }
+    }
+  }
   // kEpiResStats: the residual rows of the wave's first stripe (and their
   // LayerNorm statistics) are loaded into registers under the main loop,
   // issued right after the first slices; those of its other stripes right
@@ -530,7 +556,6 @@ void gemm_mfma_kernel(GemmParams p) {
                       WM == 4 && WN == 2, "fused QKV attention tile");
     constexpr int HD = 64;
     f16 *qkv = (f16 *)smem;  // 3 x 256 x 64 halves = 96 KB, inside the ring
-    const f16 *bias = (const f16 *)p.bias;
     const int h32 = lane >> 5;
     // With ln_part the rows of X are the LayerNorm input: Q, K, V are
     // rstd (acc - mean s) + c (see GemmParams), (mean, rstd) per row in LDS.
@@ -557,8 +582,7 @@ void gemm_mfma_kernel(GemmParams p) {
       for (int j = 0; j < TN; ++j) {
         const int cb = wn * WTN + j * 32;  // first tile column of the block
         const int d = cb % HD + (lane & 31), n = n0 + cb + (lane & 31);
-        const float sv = ln ? p.ln_s[n] : 0.f;
-        const float cv = ln ? p.ln_c[n] : to_f(bias[n]);
+        const float sv = col_s[j], cv = col_c[j];  // column n's constants
         f16 *dst = qkv + (cb / HD) * (BM * HD);
         // one formula for both cases (no per-element select): without ln,
         // (mean, rstd) = (0, 1) and sv = 0 make it fma(1, fma(-0, 0, acc), c),
@@ -632,28 +656,14 @@ void gemm_mfma_kernel(GemmParams p) {
     // int8 output (re-quantisation): bias and residual are fp16; the value is
     // rounded to fp16 first, so the result equals quantising the fp16 output.
     constexpr bool Q8 = std::is_same<OutT, int8_t>::value;
-    typedef typename std::conditional<Q8, f16, OutT>::type BiasT;
     OutT *C = (OutT *)p.C + (p.splits > 1 ? split * p.split_stride : 0);
-    const BiasT *bias = (const BiasT *)p.bias;
     const BiasT *res = (const BiasT *)p.res;
     const float inv_q = Q8 ? 1.0f / p.s_q : 1.0f;
     const bool vec_ok = (p.ldc % 8 == 0) && (Q8 ? aligned8(p.C) : aligned16(p.C)) &&
                         (!RESID || ((p.ldr % 8 == 0) && aligned16(p.res)));
-    float bj[TN], sj[TN];
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int col = n0 + wn * WTN + j * MS + frow;
-      bj[j] = 0.f;
-      sj[j] = 1.f;
-      if (col < p.N) {
-        if (EPI != ZK_EPI_NONE && !LN_IN) bj[j] = to_f(bias[col]);
-        if (DEQ) sj[j] = p.s_x * p.s_w[col];
-        if (LN_IN) {  // column sum of W' and offset for this lane's column
-          sj[j] = p.ln_s[col];
-          bj[j] = p.ln_c[col];
-        }
-      }
-    }
+    // this lane's column constants, loaded at kernel start: bias (or LN_IN's
+    // offset c) and scale (DEQ's s_x s_w, LN_IN's column sum s)
+    const float *bj = col_c, *sj = col_s;
     // the residual's value at (row, col) (RES_STATS with res_ln: its LayerNorm)
     auto resid = [&](int row, int col, float r) {
       if constexpr (RES_STATS) {
