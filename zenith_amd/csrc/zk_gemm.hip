@@ -390,6 +390,33 @@ void gemm_mfma_kernel(GemmParams p) {
       res_ms[i][k] = lb[in && p.res_ln ? row : 0];
     }
   };
+  // With res_ln, the residual LayerNorm's gamma and beta at this lane's
+  // vector columns (the same for every stripe of the wave), all loaded
+  // before any epilogue store (a load issued after a store could only be
+  // waited for together with that store). The fp16 4-wave tiles (one wave
+  // per SIMD, registers to spare) load them here, at kernel start, so that
+  // their latency passes under the main loop; the others after it.
+  constexpr bool EARLY_GB = RES_PREF && WM * WN == 4 && std::is_same<OP, F16Op>::value;
+  f16x8 res_g[NPV], res_b[NPV];
+  auto load_gb = [&]() {
+#pragma unroll
+    for (int k = 0; k < NPV; ++k) {
+      const int col = n0 + wn * WTN + ((lane + 64 * k) % (WTN / 8)) * 8;
+      const int64_t c = col + 8 <= p.N ? col : 0;
+      res_g[k] = *(const f16x8 *)((const f16 *)p.res_gamma + c);
+      res_b[k] = *(const f16x8 *)((const f16 *)p.res_beta + c);
+    }
+  };
+  if constexpr (EARLY_GB) {
+    if (p.res_ln) load_gb();
+  }
+  // The fused attention's sequence length for this wave's queries, loaded
+  // at kernel start for the same reason.
+  int attn_len = 0;
+  if constexpr (EPI == kEpiQkvAttn) {
+    const int b = m0 / p.seq + wave * 32 / p.seq;
+    attn_len = p.valid_lens && b < p.batch ? p.valid_lens[b] : p.seq;
+  }
   const int kbytes = p.K * OP::kElem;
   const int64_t lda_b = p.lda * OP::kElem, ldb_b = p.ldb * OP::kElem;
   const int a_rows = min(BM, p.M - m0), b_rows = min(BN, p.N - n0);
@@ -527,23 +554,10 @@ void gemm_mfma_kernel(GemmParams p) {
     mma_step(1);
   }
 #undef ZK_ISSUE
-  // With res_ln, the residual LayerNorm's gamma and beta at this lane's
-  // vector columns (the same for every stripe of the wave), loaded together
-  // before any epilogue store: a load issued after a store could only be
-  // waited for together with that store.
-  f16x8 res_g[NPV], res_b[NPV];
   if constexpr (RES_PREF) {
 #pragma unroll
     for (int i = 1; i < NPT; ++i) load_res(i);
-    if (p.res_ln) {
-#pragma unroll
-      for (int k = 0; k < NPV; ++k) {
-        const int col = n0 + wn * WTN + ((lane + 64 * k) % (WTN / 8)) * 8;
-        const int64_t c = col + 8 <= p.N ? col : 0;
-        res_g[k] = *(const f16x8 *)((const f16 *)p.res_gamma + c);
-        res_b[k] = *(const f16x8 *)((const f16 *)p.res_beta + c);
-      }
-    }
+    if (!EARLY_GB && p.res_ln) load_gb();
   }
   __syncthreads();  // every wave is done reading the ring; it becomes epilogue space
   if constexpr (EPI == kEpiQkvAttn) {
@@ -603,7 +617,7 @@ void gemm_mfma_kernel(GemmParams p) {
     const int sq = wave * 32 / p.seq;
     const int b = m0 / p.seq + sq;
     if (b < p.batch) {
-      int L = p.valid_lens ? p.valid_lens[b] : p.seq;
+      int L = attn_len;
       L = L < 0 ? 0 : (L > p.seq ? p.seq : L);
       f16x8 qf[HD / 16];
 #pragma unroll
