@@ -161,15 +161,23 @@ __device__ __forceinline__ void attn32_softmax(f32x16 (&s)[2], int t, int L, flo
   }
   // with m = -inf every score of this query is -inf so far: exp2 gives 0
   const float mneg = MASK && m == -__builtin_inff() ? 0.0f : -m;
-  float psum = 0.f;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float e = __builtin_amdgcn_exp2f(fmaf(s[kb][r], scale_log2, mneg));
-      psum += e;
-      pf[kb][r >> 3][r & 7] = (f16)e;
-    }
+    for (int r = 0; r < 16; ++r)
+      pf[kb][r >> 3][r & 7] = (f16)__builtin_amdgcn_exp2f(fmaf(s[kb][r], scale_log2, mneg));
+  // the row sum of the probabilities as rounded to fp16 (the P the P.V
+  // product uses), two at a time with v_dot2_f32_f16 against (1, 1)
+  float psum = 0.f;
+  const f16x2 one2 = {(f16)1.0f, (f16)1.0f};
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2)
+#pragma unroll
+      for (int e = 0; e < 8; e += 2)
+        psum = __builtin_amdgcn_fdot2(f16x2{pf[kb][c2][e], pf[kb][c2][e + 1]}, one2, psum,
+                                      false);
   {
     float a, b;
     half_swap(psum, a, b);
