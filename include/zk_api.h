@@ -383,11 +383,12 @@ int zk_gemm_f16_ws(const void *A, const void *B, void *C, int64_t M, int64_t N,
  * bit-identical to zk_gemm_f16_ws (ZK_EPI_BIAS, fp16 out, ldc = N) into T
  * followed by zk_layernorm(T, R). When the product splits along K (a
  * workspace of at least zk_gemm_workspace_size(M, N, K, ZK_F16) bytes, as
- * for zk_gemm_f16_ws) into at most M / 32 splits, and N is a multiple of 8
- * up to 8192 with 16-byte aligned bias, R, gamma, beta and Y, the split
- * partials are read straight by the LayerNorm launch, which forms the rows
- * of T itself: one launch fewer, and T is not written. Otherwise T ([M, N]
- * fp16, contiguous) holds the product as the pair would leave it. R, Y: [M, N] contiguous; bias,
+ * for zk_gemm_f16_ws), N is a multiple of 8 with 16-byte aligned bias, R,
+ * gamma, beta and Y, and either M < 2048 with N <= 1024 or at most M / 32
+ * splits with N <= 8192, the split partials are read straight by the
+ * LayerNorm launch, which forms the rows of T itself: one launch fewer, and
+ * T is not written. Otherwise T ([M, N] fp16, contiguous) holds the product
+ * as the pair would leave it. R, Y: [M, N] contiguous; bias,
  * gamma, beta: [N]. Operand rules of zk_gemm_f16 (W as [N, K], K, lda, ldw
  * multiples of 8, A and W 16-byte aligned). No single reference
  * counterpart: the out-projection / FFN-down linear and the Add+LayerNorm

@@ -297,13 +297,13 @@ def test_linear_f32_c_abi(dev, M, K, N, epi):
                                        (128, 768, 768, 0), (512, 768, 768, 0),
                                        (256, 3072, 768, 192), (4096, 768, 768, 0),
                                        (96, 1000, 200, 24), (37, 3072, 96, 0),
-                                       (320, 1024, 64, 8)])
+                                       (320, 1024, 64, 8), (2048, 3072, 64, 0)])
 def test_gemm_add_layernorm(dev, M, K, N, pad):
     """zk_gemm_f16_add_ln = the pair it replaces, bit for bit: zk_gemm_f16_ws
     (bias epilogue, fp16 out) into T, then zk_layernorm(T, R). Products that
-    split along K into at most M / 32 splits take the fused path (the
-    LayerNorm launch sums the split partials itself), the others the pair;
-    both against the float64 product
+    split along K take the fused path (the LayerNorm launch sums the split
+    partials itself: four wavefronts per row below 2048 rows, one with at
+    least 32 rows per split otherwise), the others the pair; both against the float64 product
     and the oracle's Add+LayerNorm at the fp16 bar. A and W with padded rows
     (the encoder's FFN intermediate), K not a multiple of the 128-byte slice
     (1000), N a multiple of 8 only (200, 96) and a ragged M (37)."""
@@ -337,8 +337,12 @@ def test_gemm_add_layernorm(dev, M, K, N, pad):
            tg.data_ptr(), tbe.data_ptr(), t_buf.data_ptr(), y.data_ptr(), M, N, K, tx.stride(0),
            tw.stride(0), 1e-12, ws.data_ptr(), need, s)
     torch.cuda.synchronize()
-    # split products of at least 32 rows per split read the partials in the LayerNorm launch
-    fused = need > 0 and need // (M * N * 4) * 32 <= M
+    # split products read the partials in the LayerNorm launch: four
+    # wavefronts per row below 2048 rows of at most 1024 values, else one
+    # wavefront per row with at least 32 rows per split
+    splits = need // (M * N * 4)
+    wide = M < 2048 and N <= 1024
+    fused = need > 0 and (wide or splits * 32 <= M)
     assert torch.equal(y, y_pair), (M, K, N)
     if not fused:
         assert torch.equal(t_buf, t_pair)
@@ -346,5 +350,7 @@ def test_gemm_add_layernorm(dev, M, K, N, pad):
     ref = ops.add_layernorm(t_ref, r, g, be, 1e-12)
     ok, worst = fp16_tol(y.float().cpu().numpy(), ref)
     assert ok, worst
-    print(f"gemm+add+LN M={M} K={K} N={N}: {'fused over split partials' if fused else 'pair'}, "
+    kind = ("pair" if not fused else "partials, four wavefronts per row" if wide
+            else "partials, one wavefront per row")
+    print(f"gemm+add+LN M={M} K={K} N={N}: {kind}, "
           f"bit-identical to the pair", flush=True)

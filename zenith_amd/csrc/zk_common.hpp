@@ -60,11 +60,14 @@ int gemm_f16_impl(const void *A, const void *B, void *C, int64_t M, int64_t N, i
 // splitk_reduce (ZK_EPI_BIAS) followed by zk_layernorm. ln_partials_ok says
 // whether the shape and alignments allow it (hidden a multiple of 8 up to
 // 8192, 16-byte aligned operands).
+// With `wide` (allowed when ln_partials_wide_ok) each row gets a workgroup
+// of four wavefronts to form it from the partials.
 bool ln_partials_ok(const float *ws, int64_t stride, const void *bias, const void *res,
                     const void *g, const void *b, const void *y, int64_t rows, int64_t hidden);
+bool ln_partials_wide_ok(int64_t rows, int64_t hidden);
 int ln_add_partials_f16(const float *ws, int splits, int64_t stride, const void *bias,
                         const void *res, const void *g, const void *b, void *y, int64_t rows,
-                        int64_t hidden, float eps, hipStream_t s);
+                        int64_t hidden, float eps, bool wide, hipStream_t s);
 
 // Symmetric int8 quantisation of one value,
 //   q = clamp(round_half_even(RN(x / scale)), -128, 127)

@@ -1272,13 +1272,12 @@ extern "C" int zk_gemm_f16_ws(const void *A, const void *B, void *C, int64_t M, 
 // rows the wave LayerNorm can hold) runs as its split partials plus one
 // LayerNorm launch that forms the rows from the partials; anything else as
 // zk_gemm_f16_ws into T followed by zk_layernorm. Both give the pair's
-// result bit for bit. The LayerNorm launch has one wavefront per row, each
-// reading its row's partials of every split: that pays while there are at
-// least 32 rows per split. BERT encoder per step (12 layers, s128), pair ->
-// partials read by the LayerNorm: b2 (out-projection and FFN-down in 5
-// splits) 0.635 -> 0.617 ms, b4 (2 and 4 splits) 0.675 -> 0.643 ms; at b1
-// (6 and 10 splits of 128 rows) it was 0.604 -> 0.621 ms, so b1 keeps the
-// pair, whose reduction spreads over many more workgroups.
+// result bit for bit. Below 2048 rows of at most 1024 values each row gets a
+// workgroup of four wavefronts to form it (BERT encoder per step, s128,
+// pair -> partials: b1 0.602 -> 0.555 ms, b2 0.635 -> 0.581, b4 0.679 ->
+// 0.626); otherwise one wavefront per row reads every split of its row,
+// which needs at least 32 rows per split to pay (with it b1, 6 and 10
+// splits of 128 rows, measured 0.604 -> 0.621 ms, b2 0.617, b4 0.646).
 extern "C" int zk_gemm_f16_add_ln(const void *A, const void *W, const void *bias, const void *R,
                                   const void *gamma, const void *beta, void *T, void *Y,
                                   int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw,
@@ -1300,7 +1299,8 @@ extern "C" int zk_gemm_f16_add_ln(const void *A, const void *W, const void *bias
   hipStream_t s = as_stream(stream);
   const SplitPlan sp = plan_split(M, N, K, 2);
   const float *ws = (const float *)workspace;
-  if (ws && sp.splits > 1 && ws_bytes >= split_ws_bytes(M, N, sp) && sp.splits * 32 <= M &&
+  const bool wide = ln_partials_wide_ok(M, N), narrow = !wide && sp.splits * 32 <= M;
+  if (ws && sp.splits > 1 && ws_bytes >= split_ws_bytes(M, N, sp) && (narrow || wide) &&
       ln_partials_ok(ws, M * N, bias, R, gamma, beta, Y, M, N)) {
     GemmParams q{A, W, workspace, (int)M, (int)N, (int)K, lda, ldw, N, nullptr, nullptr, 0, 1.f,
                  nullptr, 0};
@@ -1310,7 +1310,7 @@ extern "C" int zk_gemm_f16_add_ln(const void *A, const void *W, const void *bias
     if (!launch_mfma<F16Op, float, false>(q, ZK_EPI_NONE, s, 3))
       return fail(ZK_ERR_UNSUPPORTED, "%s: no partial-product kernel for this shape", who);
     if ((st = check_launch(who))) return st;
-    return ln_add_partials_f16(ws, sp.splits, M * N, bias, R, gamma, beta, Y, M, N, eps, s);
+    return ln_add_partials_f16(ws, sp.splits, M * N, bias, R, gamma, beta, Y, M, N, eps, wide, s);
   }
   st = gemm_f16_impl(A, W, T, M, N, K, lda, ldw, N, 1, ZK_F16, bias, nullptr, 0, ZK_EPI_BIAS,
                      workspace, ws_bytes, stream);

@@ -33,10 +33,15 @@ template <typename T> struct ResLn {
   const T *g, *b;    // [hidden]
 };
 
-// PART: the input rows are not read from x but formed from the fp32 split-K
-// partials of a GEMM, [splits][rows][hidden] (split s at ws + s * stride),
-// summed in split order from zero, plus the bias, rounded to T: exactly the
-// values splitk_reduce (epilogue ZK_EPI_BIAS) would store for x.
+// PART (1 or 2): the input rows are not read from x but formed from the fp32
+// split-K partials of a GEMM, [splits][rows][hidden] (split s at ws + s *
+// stride), summed in split order from zero, plus the bias, rounded to T:
+// exactly the values splitk_reduce (epilogue ZK_EPI_BIAS) would store for x.
+// PART 1: each lane forms its own vectors. PART 2 (rows of at most 1024
+// values, LPR = 64): one row per workgroup, whose four wavefronts form the
+// row in LDS, after which wavefront 0 alone runs the LayerNorm on it, with
+// the same arithmetic as for a row read from memory; for many splits of few
+// rows, where one wavefront reading every split of its row is too slow.
 template <typename T> struct PartIn {
   const float *ws;
   int splits;
@@ -48,7 +53,7 @@ template <typename T> struct PartIn {
 // 16-byte vectors, so two rows per wavefront give every lane exactly three.
 // Q8: also write q = quant(y) as int8 (the fp16 output value quantised with
 // scale qs), for an int8 GEMM that consumes the normalised rows.
-template <typename T, int MAXV, int RES, int LPR, bool Q8, bool PART = false>
+template <typename T, int MAXV, int RES, int LPR, bool Q8, int PART = 0>
 __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
     const T *__restrict__ x, const T *__restrict__ res,
     const T *__restrict__ gamma, const T *__restrict__ beta, T *__restrict__ y,
@@ -60,11 +65,28 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
   constexpr int RPW = kWave / LPR;  // rows per wavefront
   const int lane = threadIdx.x & (kWave - 1);
   const int sub = lane % LPR;
-  const int64_t row = ((int64_t)blockIdx.x * kLnWaves + (threadIdx.x >> 6)) * RPW + lane / LPR;
+  const int64_t row = PART == 2
+                          ? (int64_t)blockIdx.x
+                          : ((int64_t)blockIdx.x * kLnWaves + (threadIdx.x >> 6)) * RPW + lane / LPR;
   // Rows past the end load nothing and store nothing, but stay in the
   // shuffles (their partner lanes belong to the same row group).
   const bool live = row < rows;
   const int nvec = hidden / W;
+  __shared__ V prow[PART == 2 ? 128 : 1];
+  if constexpr (PART == 2) {
+    static_assert(W == 8 && LPR == kWave && MAXV <= 2, "one wavefront per row of <= 128 vectors");
+    // the row's values from the partials, four columns per thread
+    const float *pp = pin.ws + row * hidden;
+    for (int c = threadIdx.x; c < hidden / 4; c += kLnWaves * kWave) {
+      f32x4 t = {0.f, 0.f, 0.f, 0.f};
+      for (int sp = 0; sp < pin.splits; ++sp) t += *(const f32x4 *)(pp + sp * pin.stride + 4 * c);
+      f16 *dst = reinterpret_cast<f16 *>(prow) + 4 * c;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dst[j] = (T)(t[j] + (float)pin.bias[4 * c + j]);
+    }
+    __syncthreads();
+    if (threadIdx.x >= kWave) return;
+  }
   const V *xr = reinterpret_cast<const V *>(x + (live ? row : 0) * hidden);
   const V *rr = reinterpret_cast<const V *>(res + (RES != kResNone && live ? row * hidden : 0));
   float2 rms = make_float2(0.f, 1.f);
@@ -77,7 +99,9 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
     const int idx = sub + k * LPR;
     if (live && idx < nvec) {
       V a;
-      if constexpr (PART) {
+      if constexpr (PART == 2) {
+        a = prow[idx];
+      } else if constexpr (PART == 1) {
         static_assert(W == 8, "partials are summed 8 columns at a time");
         const float *pp = pin.ws + (row * hidden + (int64_t)idx * W);
         float t[W] = {};
@@ -313,18 +337,31 @@ bool ln_partials_ok(const float *ws, int64_t stride, const void *bias, const voi
          aligned16(res) && aligned16(g) && aligned16(b) && aligned16(y);
 }
 
+bool ln_partials_wide_ok(int64_t rows, int64_t hidden) {
+  return rows < 2048 && hidden <= 1024;  // ln_pick's one-wavefront-per-row shapes
+}
+
 int ln_add_partials_f16(const float *ws, int splits, int64_t stride, const void *bias,
                         const void *res, const void *g, const void *b, void *y, int64_t rows,
-                        int64_t hidden, float eps, hipStream_t s) {
+                        int64_t hidden, float eps, bool wide, hipStream_t s) {
   const PartIn<f16> pin{ws, splits, stride, (const f16 *)bias};
   const int h = (int)hidden;
   ln_pick(rows, hidden / 8, [&](auto mv, auto lpr) {
     constexpr int MV = decltype(mv)::value, LPR = decltype(lpr)::value;
     constexpr int rows_per_block = kLnWaves * (kWave / LPR);
+    const ResLn<f16> none{nullptr, nullptr, nullptr};
+    if constexpr (LPR == kWave && MV <= 2) {
+      if (wide) {
+        ln_wave_kernel<f16, MV, kResPre, LPR, false, 2><<<(unsigned)rows, kLnWaves * kWave, 0, s>>>(
+            nullptr, (const f16 *)res, (const f16 *)g, (const f16 *)b, (f16 *)y, nullptr, 1.f,
+            rows, h, eps, none, pin);
+        return;
+      }
+    }
     const unsigned grid = (unsigned)((rows + rows_per_block - 1) / rows_per_block);
-    ln_wave_kernel<f16, MV, kResPre, LPR, false, true><<<grid, kLnWaves * kWave, 0, s>>>(
+    ln_wave_kernel<f16, MV, kResPre, LPR, false, 1><<<grid, kLnWaves * kWave, 0, s>>>(
         nullptr, (const f16 *)res, (const f16 *)g, (const f16 *)b, (f16 *)y, nullptr, 1.f, rows,
-        h, eps, ResLn<f16>{nullptr, nullptr, nullptr}, pin);
+        h, eps, none, pin);
   });
   return check_launch("zk_gemm_f16_add_ln");
 }
