@@ -140,6 +140,7 @@ def kernel_cases(torch, dev):
 
     from zenith_amd import _lib as L
     from zenith_amd import synthetic
+    from zenith_amd.encoder import FFN_PAD
 
     lib = L.load()
     s = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
@@ -273,12 +274,16 @@ def kernel_cases(torch, dev):
                 f"B={B} S={S} heads={heads} M={B * S} K={H} N={3 * H} + attention (dense FLOPs)"
         return setup
 
-    def res_stats(M, K, N, ln_res=True):
+    def res_stats(M, K, N, ln_res=True, pad=0):
         """The encoder's out-projection / FFN-down with the folded LayerNorm:
-        bias + residual (LayerNorm-ed on the fly) + row statistics."""
+        bias + residual (LayerNorm-ed on the fly) + row statistics. pad: extra
+        elements per A and W row, as the encoder lays out the FFN
+        intermediate and the FFN-down weight."""
         def setup():
-            a = torch.from_numpy(synthetic.uniform((M, K), tag=1)).to(dev, f16)
-            w = torch.from_numpy(synthetic.uniform((N, K), tag=2)).to(dev, f16) * 0.05
+            a = torch.zeros((M, K + pad), dtype=f16, device=dev)
+            a[:, :K] = torch.from_numpy(synthetic.uniform((M, K), tag=1)).to(dev, f16)
+            w = torch.zeros((N, K + pad), dtype=f16, device=dev)
+            w[:, :K] = torch.from_numpy(synthetic.uniform((N, K), tag=2)).to(dev, f16) * 0.05
             b = torch.zeros(N, dtype=f16, device=dev)
             r = torch.from_numpy(synthetic.normal((M, N), tag=3)).to(dev, f16)
             c = torch.empty((M, N), dtype=f16, device=dev)
@@ -288,17 +293,20 @@ def kernel_cases(torch, dev):
             be = torch.zeros(N, dtype=f16, device=dev)
             part = torch.empty((M, N // 96, 2), dtype=torch.float32, device=dev)
             keep = (a, w, b, r, c, ms, g, be, part)
-            args = (a.data_ptr(), w.data_ptr(), c.data_ptr(), M, N, K, K, K, N, b.data_ptr(),
-                    r.data_ptr(), N, ms.data_ptr() if ln_res else None,
+            args = (a.data_ptr(), w.data_ptr(), c.data_ptr(), M, N, K, K + pad, K + pad, N,
+                    b.data_ptr(), r.data_ptr(), N, ms.data_ptr() if ln_res else None,
                     g.data_ptr() if ln_res else None, be.data_ptr() if ln_res else None,
                     part.data_ptr())
+            rows = f", A and W rows of {2 * (K + pad)} bytes as in the encoder" if pad else ""
             return (lambda i: _rc(L, lib.zk_gemm_f16_res_stats(*args, s())) and keep), \
                 2.0 * M * N * K, "TFLOP/s", "fp16", "mfma", \
-                f"M={M} K={K} N={N} + residual LayerNorm + row statistics"
+                f"M={M} K={K} N={N} + residual LayerNorm + row statistics{rows}"
         return setup
 
-    def gemm_ln(M, K, N, gelu):
-        """The encoder's FFN-up with the folded LayerNorm of its input."""
+    def gemm_ln(M, K, N, gelu, pad=0):
+        """The encoder's FFN-up with the folded LayerNorm of its input. pad:
+        extra elements per output row, as the encoder lays out the FFN
+        intermediate."""
         def setup():
             a = torch.from_numpy(synthetic.normal((M, K), tag=1)).to(dev, f16)
             w = torch.from_numpy(synthetic.uniform((N, K), tag=2)).to(dev, f16) * 0.05
@@ -306,15 +314,16 @@ def kernel_cases(torch, dev):
             part[..., 1] = 96.0
             sc = torch.zeros(N, dtype=torch.float32, device=dev)
             cc = torch.zeros(N, dtype=torch.float32, device=dev)
-            c = torch.empty((M, N), dtype=f16, device=dev)
+            c = torch.empty((M, N + pad), dtype=f16, device=dev)
             mr = torch.empty((M, 2), dtype=torch.float32, device=dev)
             keep = (a, w, part, sc, cc, c, mr)
-            args = (a.data_ptr(), w.data_ptr(), c.data_ptr(), M, N, K, K, K, N, part.data_ptr(),
+            args = (a.data_ptr(), w.data_ptr(), c.data_ptr(), M, N, K, K, K, N + pad, part.data_ptr(),
                     1e-12, sc.data_ptr(), cc.data_ptr(), mr.data_ptr(),
                     L.ZK_EPI_BIAS_GELU_ERF if gelu else L.ZK_EPI_BIAS)
             return (lambda i: _rc(L, lib.zk_gemm_f16_ln(*args, s())) and keep), \
                 2.0 * M * N * K, "TFLOP/s", "fp16", "mfma", \
-                f"M={M} K={K} N={N} on LayerNorm-ed rows (folded)" + (" + GELU" if gelu else "")
+                f"M={M} K={K} N={N} on LayerNorm-ed rows (folded)" + (" + GELU" if gelu else "") + \
+                (f", output rows of {2 * (N + pad)} bytes as in the encoder" if pad else "")
         return setup
 
     def qkv_attn_ln(B=32, S=128, heads=12):
@@ -427,8 +436,8 @@ def kernel_cases(torch, dev):
         # the four launches of an encoder layer at b32 s128 (LayerNorms folded)
         "qkv_attn_ln_s128": qkv_attn_ln(),
         "out_proj_res_stats": res_stats(4096, 768, 768),
-        "ffn_up_ln": gemm_ln(4096, 768, 3072, True),
-        "ffn_down_res_stats": res_stats(4096, 3072, 768),
+        "ffn_up_ln": gemm_ln(4096, 768, 3072, True, pad=FFN_PAD),
+        "ffn_down_res_stats": res_stats(4096, 3072, 768, pad=FFN_PAD),
         "attn_s512": attn(512),
         "int8_ffn_up": gemm_i8(4096, 768, 3072, L.ZK_EPI_BIAS_GELU_ERF, requant=True),
         "int8_ffn_down": gemm_i8(4096, 3072, 768, E),
