@@ -102,11 +102,15 @@ __device__ __forceinline__ void half_swap(float x, float &a, float &b) {
 // online-softmax update of the running max m and sum l (lazy rescaling of
 // o), and the probabilities as fp16 B fragments pf of the P.V product. t is
 // the tile index (keys t*64 ..); mp / mrow are read only with MASK.
+// It runs as two parts: attn32_softmax_max (masking, the tile max and the
+// lazy rescale; returns the exponent offset) and attn32_softmax_exp (the
+// probabilities and the row sum), so that a caller can place independent
+// MFMAs among the second part's VALU work.
 template <int D, bool MASK>
-__device__ __forceinline__ void attn32_softmax(f32x16 (&s)[2], int t, int L, float scale_log2,
-                                               const AttnParams *mp, const uint8_t *mrow,
-                                               int lane, f32x16 (&o)[D / 32], float &m,
-                                               float &l, f16x8 (&pf)[2][2]) {
+__device__ __forceinline__ float attn32_softmax_max(f32x16 (&s)[2], int t, int L,
+                                                    float scale_log2, const AttnParams *mp,
+                                                    const uint8_t *mrow, int lane,
+                                                    f32x16 (&o)[D / 32], float &m, float &l) {
   constexpr int KT = 64;
   const int h32 = lane >> 5;
   // Tile max on the raw scores (the scale is positive), masking only the
@@ -160,7 +164,12 @@ __device__ __forceinline__ void attn32_softmax(f32x16 (&s)[2], int t, int L, flo
       for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
   }
   // with m = -inf every score of this query is -inf so far: exp2 gives 0
-  const float mneg = MASK && m == -__builtin_inff() ? 0.0f : -m;
+  return MASK && m == -__builtin_inff() ? 0.0f : -m;
+}
+
+template <int D>
+__device__ __forceinline__ void attn32_softmax_exp(const f32x16 (&s)[2], float scale_log2,
+                                                   float mneg, float &l, f16x8 (&pf)[2][2]) {
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -183,6 +192,15 @@ __device__ __forceinline__ void attn32_softmax(f32x16 (&s)[2], int t, int L, flo
     half_swap(psum, a, b);
     l += a + b;  // the same sum in either order (fp32 addition commutes)
   }
+}
+
+template <int D, bool MASK>
+__device__ __forceinline__ void attn32_softmax(f32x16 (&s)[2], int t, int L, float scale_log2,
+                                               const AttnParams *mp, const uint8_t *mrow,
+                                               int lane, f32x16 (&o)[D / 32], float &m,
+                                               float &l, f16x8 (&pf)[2][2]) {
+  const float mneg = attn32_softmax_max<D, MASK>(s, t, L, scale_log2, mp, mrow, lane, o, m, l);
+  attn32_softmax_exp<D>(s, scale_log2, mneg, l, pf);
 }
 
 // Phase 3, attn32_pv: O^T[d][q] += V^T[d][key] . P^T[key][q] from the V

@@ -630,10 +630,36 @@ void gemm_mfma_kernel(GemmParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
       float m = -__builtin_inff(), l = 0.f;
+      // At most two 64-key tiles (sequences of 64 or 128 tokens), both in
+      // LDS: the second tile's Q.K^T is issued before the first tile's
+      // softmax, so that its MFMAs can run under that VALU work (the same
+      // arithmetic per tile as attn32_tile, in the same order).
       const int ntiles = (L + 63) / 64;
-      for (int t = 0; t < ntiles; ++t)
-        attn32_tile<HD, true, HD, false>(Kt + t * 64 * HD, Vt + t * 64 * HD, qf, t, L,
-                                         p.scale_log2, nullptr, nullptr, lane, o, m, l);
+      if (ntiles > 0) {
+        f32x16 s0[2], s1[2];
+        f16x8 pf[2][2];
+        attn32_qk<HD, true, HD>(Kt, qf, lane, s0);
+        const float mneg = attn32_softmax_max<HD, false>(s0, 0, L, p.scale_log2, nullptr,
+                                                         nullptr, lane, o, m, l);
+        // The second tile's 8 K-fragment reads and 8 MFMAs, interleaved with
+        // the first tile's exponentials. They are issued whatever the
+        // length (a wave-uniform branch here would let the compiler hoist the
+        // exponentials above it); with 64-token sequences they recompute
+        // tile 0 into s1, which is not used.
+        attn32_qk<HD, true, HD>(Kt + (p.seq > 64 ? 64 * HD : 0), qf, lane, s1);
+        attn32_softmax_exp<HD>(s0, p.scale_log2, mneg, l, pf);
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // DS reads
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x402, 8, 0);  // VALU incl. exp
+        }
+        attn32_pv<HD, true, HD>(Vt, pf, lane, o);
+        if (ntiles > 1) {
+          attn32_softmax<HD, false>(s1, 1, L, p.scale_log2, nullptr, nullptr, lane, o, m, l, pf);
+          attn32_pv<HD, true, HD>(Vt + 64 * HD, pf, lane, o);
+        }
+      }
       const int grow = m0 + qr;
       if (grow < p.M) {
         const float inv = l > 0.f ? 1.0f / l : 0.f;
