@@ -126,6 +126,15 @@ __device__ __forceinline__ u32x2 quant8(const float (&x)[8], float scale, float 
 }
 
 // ------------------------------------------------------------ device math --
+// x as an fp32 value in a register: the compiler may otherwise fuse the fma
+// that produced it with a following conversion to fp16 (v_fma_mix*_f16,
+// one rounding where the source has two, to fp32 and then to fp16), and
+// whether it does depends on the surrounding code, so two kernels with the
+// same arithmetic could round a few values differently.
+__device__ __forceinline__ float as_f32(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
 __device__ __forceinline__ float gelu_erf(float x) {
   // 0.5 x (1 + erf(x / sqrt(2)))
   return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));

@@ -1066,7 +1066,7 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ w
     for (int sp = 0; sp < splits; ++sp) v += ws[sp * stride + i];
     v = epilogue<EPI>(v, EPI != ZK_EPI_NONE ? to_f(bias[n]) : 0.f);
     if (EPI == ZK_EPI_BIAS_RESIDUAL) v += to_f(res[m * ldr + n]);
-    C[m * ldc + n] = (OutT)v;
+    C[m * ldc + n] = (OutT)as_f32(v);  // rounded to fp32, then to OutT, as the GEMM epilogue
   }
 }
 
@@ -1093,7 +1093,7 @@ __global__ __launch_bounds__(256) void splitk_reduce4(const float *__restrict__ 
     for (int k = 0; k < 4; ++k) {
       float t = epilogue<EPI>(v[k], EPI != ZK_EPI_NONE ? to_f(b4[k]) : 0.f);
       if (EPI == ZK_EPI_BIAS_RESIDUAL) t += to_f(r4[k]);
-      o4[k] = (OutT)t;
+      o4[k] = (OutT)as_f32(t);
     }
     *(OutT4 *)(C + m * ldc + n) = o4;
   }

@@ -19,6 +19,9 @@ template <> struct LnVec<f16> { typedef f16x8 type; static constexpr int n = 8; 
 template <> struct LnVec<float> { typedef f32x4 type; static constexpr int n = 4; };
 
 constexpr int kLnWaves = 4;  // wavefronts per 256-thread block
+// launches of at most this many wavefronts (16 per CU) read their rows with
+// the loads batched (ln_wave_kernel's BATCH)
+constexpr int kLnBatchWaves = 4096;
 
 // Residual placement: none, added before the statistics (Add+LayerNorm),
 // added to the normalised output (LayerNorm+Add), or added before the
@@ -53,7 +56,7 @@ template <typename T> struct PartIn {
 // 16-byte vectors, so two rows per wavefront give every lane exactly three.
 // Q8: also write q = quant(y) as int8 (the fp16 output value quantised with
 // scale qs), for an int8 GEMM that consumes the normalised rows.
-template <typename T, int MAXV, int RES, int LPR, bool Q8, int PART = 0>
+template <typename T, int MAXV, int RES, int LPR, bool Q8, int PART = 0, bool BATCH = false>
 __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
     const T *__restrict__ x, const T *__restrict__ res,
     const T *__restrict__ gamma, const T *__restrict__ beta, T *__restrict__ y,
@@ -92,52 +95,115 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
   float2 rms = make_float2(0.f, 1.f);
   if constexpr (RES == kResPreLn) rms = rl.ms[live ? row : 0];
 
+  const V *gv = reinterpret_cast<const V *>(gamma);
+  const V *bv = reinterpret_cast<const V *>(beta);
+  // BATCH (rows read from memory, launches of at most kLnBatchWaves
+  // wavefronts): loads are issued ahead of their use, each from a valid
+  // address (row 0, vector 0 where the lane has nothing to read): the row's
+  // vectors (and residual) four at a time, and, for rows of at most four
+  // vectors per lane, the output's gamma / beta (and post residual) at the
+  // start, so that a wavefront waits for memory about once rather than once
+  // per load. In a launch of one round of wavefronts that wait is the
+  // kernel's critical path ([4096, 768] Add+LN 6.5 -> 5.4 us); with several
+  // rounds the other wavefronts hide it, and one load at a time per
+  // wavefront was faster ([16384, 768] 13.9 us against 14.8 us batched).
+  constexpr int CH = MAXV < 4 ? MAXV : 4;
+  constexpr bool PRE_OUT = BATCH && MAXV <= 4;
+  V go[PRE_OUT ? MAXV : 1], bo[PRE_OUT ? MAXV : 1], ro[PRE_OUT && RES == kResPost ? MAXV : 1];
+  if constexpr (PRE_OUT) {
+#pragma unroll
+    for (int k = 0; k < MAXV; ++k) {
+      const int idx = sub + k * LPR, ci = idx < nvec ? idx : 0;
+      go[k] = gv[ci];
+      bo[k] = bv[ci];
+      if constexpr (RES == kResPost) ro[k] = rr[ci];
+    }
+  }
   float v[MAXV][W];
   float sum = 0.f;
+  // the input value of one vector: a (+ r, or + LN(r) with gamma rg, beta rb)
+  auto combine = [&](const V &a, const V &r, const V &rg, const V &rb, float (&f)[W]) {
 #pragma unroll
-  for (int k = 0; k < MAXV; ++k) {
-    const int idx = sub + k * LPR;
-    if (live && idx < nvec) {
-      V a;
-      if constexpr (PART == 2) {
-        a = prow[idx];
-      } else if constexpr (PART == 1) {
-        static_assert(W == 8, "partials are summed 8 columns at a time");
-        const float *pp = pin.ws + (row * hidden + (int64_t)idx * W);
-        float t[W] = {};
-        for (int sp = 0; sp < pin.splits; ++sp) {
-          const f32x4 lo = *(const f32x4 *)(pp + sp * pin.stride);
-          const f32x4 hi = *(const f32x4 *)(pp + sp * pin.stride + 4);
+    for (int j = 0; j < W; ++j) {
+      f[j] = (float)a[j];
+      if constexpr (RES == kResPre) f[j] += (float)r[j];
+      if constexpr (RES == kResPreLn)
+        f[j] += fmaf(((float)r[j] - rms.x) * rms.y, (float)rg[j], (float)rb[j]);
+    }
+  };
+  if constexpr (PART == 0 && BATCH) {
+    // Branch-free: a lane with no vector k combines what it loaded from vector
+    // 0 and keeps zeros (adding 0 leaves the sum as it is).
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            t[j] += lo[j];
-            t[j + 4] += hi[j];
-          }
+    for (int k0 = 0; k0 < MAXV; k0 += CH) {
+      V xa[CH], xq[CH], xg[CH], xb[CH];
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int idx = sub + (k0 + c) * LPR, ci = live && idx < nvec ? idx : 0;
+        xa[c] = xr[ci];
+        if constexpr (PRE) xq[c] = rr[ci];
+        if constexpr (RES == kResPreLn) {
+          xg[c] = reinterpret_cast<const V *>(rl.g)[ci];
+          xb[c] = reinterpret_cast<const V *>(rl.b)[ci];
         }
-        const V bv = reinterpret_cast<const V *>(pin.bias)[idx];
+      }
 #pragma unroll
-        for (int j = 0; j < W; ++j) a[j] = (T)(t[j] + (float)bv[j]);
+      for (int c = 0; c < CH; ++c) {
+        const int k = k0 + c;
+        const bool ok = live && sub + k * LPR < nvec;
+        float f[W];
+        combine(xa[c], xq[c], xg[c], xb[c], f);
+#pragma unroll
+        for (int j = 0; j < W; ++j) {
+          v[k][j] = ok ? f[j] : 0.f;
+          sum += v[k][j];
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < MAXV; ++k) {
+      const int idx = sub + k * LPR;
+      if (live && idx < nvec) {
+        V a;
+        if constexpr (PART == 0) {
+          a = xr[idx];
+        } else if constexpr (PART == 2) {
+          a = prow[idx];
+        } else {
+          static_assert(W == 8, "partials are summed 8 columns at a time");
+          const float *pp = pin.ws + (row * hidden + (int64_t)idx * W);
+          float t[W] = {};
+          for (int sp = 0; sp < pin.splits; ++sp) {
+            const f32x4 lo = *(const f32x4 *)(pp + sp * pin.stride);
+            const f32x4 hi = *(const f32x4 *)(pp + sp * pin.stride + 4);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              t[j] += lo[j];
+              t[j + 4] += hi[j];
+            }
+          }
+          const V bv = reinterpret_cast<const V *>(pin.bias)[idx];
+#pragma unroll
+          for (int j = 0; j < W; ++j) a[j] = (T)(t[j] + (float)bv[j]);
+        }
+        V r, rg, rb;
+        if constexpr (PRE) r = rr[idx];
+        if constexpr (RES == kResPreLn) {
+          rg = reinterpret_cast<const V *>(rl.g)[idx];
+          rb = reinterpret_cast<const V *>(rl.b)[idx];
+        }
+        float f[W];
+        combine(a, r, rg, rb, f);
+#pragma unroll
+        for (int j = 0; j < W; ++j) {
+          v[k][j] = f[j];
+          sum += f[j];
+        }
       } else {
-        a = xr[idx];
-      }
-      V r, rg, rb;
-      if (PRE) r = rr[idx];
-      if (RES == kResPreLn) {
-        rg = reinterpret_cast<const V *>(rl.g)[idx];
-        rb = reinterpret_cast<const V *>(rl.b)[idx];
-      }
 #pragma unroll
-      for (int j = 0; j < W; ++j) {
-        float f = (float)a[j];
-        if (RES == kResPre) f += (float)r[j];
-        if (RES == kResPreLn)
-          f += fmaf(((float)r[j] - rms.x) * rms.y, (float)rg[j], (float)rb[j]);
-        v[k][j] = f;
-        sum += f;
+        for (int j = 0; j < W; ++j) v[k][j] = 0.f;
       }
-    } else {
-#pragma unroll
-      for (int j = 0; j < W; ++j) v[k][j] = 0.f;
     }
   }
   auto group_sum = [](float t) {
@@ -163,22 +229,29 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
   if (!live) return;
 
   V *yr = reinterpret_cast<V *>(y + row * hidden);
-  const V *gv = reinterpret_cast<const V *>(gamma);
-  const V *bv = reinterpret_cast<const V *>(beta);
 #pragma unroll
   for (int k = 0; k < MAXV; ++k) {
     const int idx = sub + k * LPR;
     if (idx < nvec) {
-      V g = gv[idx], b = bv[idx], o;
+      V g, b, o;
+      if constexpr (PRE_OUT) {
+        g = go[k];
+        b = bo[k];
+      } else {
+        g = gv[idx];
+        b = bv[idx];
+      }
       if constexpr (RES == kResPost) {
-        const V r = rr[idx];
+        V r;
+        if constexpr (PRE_OUT) r = ro[k];
+        else r = rr[idx];
 #pragma unroll
         for (int j = 0; j < W; ++j)
-          o[j] = (T)((v[k][j] - mean) * rstd * (float)g[j] + (float)b[j] + (float)r[j]);
+          o[j] = (T)as_f32((v[k][j] - mean) * rstd * (float)g[j] + (float)b[j] + (float)r[j]);
       } else {
 #pragma unroll
         for (int j = 0; j < W; ++j)
-          o[j] = (T)((v[k][j] - mean) * rstd * (float)g[j] + (float)b[j]);
+          o[j] = (T)as_f32((v[k][j] - mean) * rstd * (float)g[j] + (float)b[j]);
       }
       store_nt(yr + idx, o);
       if constexpr (Q8) {
@@ -238,7 +311,7 @@ __global__ __launch_bounds__(256) void ln_block_kernel(
     const float f = (float)xr[i] + (PRE ? rv(i) : 0.f);
     float yv = (f - mean) * rstd * (float)gamma[i] + (float)beta[i];
     if (RES == kResPost) yv += (float)rr[i];
-    const T o = (T)yv;
+    const T o = (T)as_f32(yv);
     y[row * hidden + i] = o;
     if (Q8) q[row * hidden + i] = quant1((float)o, qs, 1.0f / qs);
   }
@@ -250,10 +323,16 @@ static void ln_wave_launch(const T *x, const T *r, const T *g, const T *b, T *y,
                            ResLn<T> rl, hipStream_t s) {
   constexpr int rows_per_block = kLnWaves * (kWave / LPR);
   const unsigned grid = (unsigned)((rows + rows_per_block - 1) / rows_per_block);
-#define ZK_LNW(RES, QQ) \
-  ln_wave_kernel<T, MAXV, RES, LPR, QQ><<<grid, kLnWaves * kWave, 0, s>>>(x, r, g, b, y, q, qs, \
-                                                                         rows, hidden, eps, rl, \
-                                                                         PartIn<T>{})
+  const bool batch = (int64_t)grid * kLnWaves <= kLnBatchWaves;
+#define ZK_LNW(RES, QQ)                                                                        \
+  do {                                                                                         \
+    if (batch)                                                                                 \
+      ln_wave_kernel<T, MAXV, RES, LPR, QQ, 0, true><<<grid, kLnWaves * kWave, 0, s>>>(        \
+          x, r, g, b, y, q, qs, rows, hidden, eps, rl, PartIn<T>{});                           \
+    else                                                                                       \
+      ln_wave_kernel<T, MAXV, RES, LPR, QQ><<<grid, kLnWaves * kWave, 0, s>>>(                 \
+          x, r, g, b, y, q, qs, rows, hidden, eps, rl, PartIn<T>{});                           \
+  } while (0)
   if (r && post) {
     if constexpr (!Q8) ZK_LNW(kResPost, false);
   } else if (r && rl.ms) {
