@@ -125,6 +125,27 @@ __device__ __forceinline__ u32x2 quant8(const float (&x)[8], float scale, float 
   return u32x2{lo ^ 0x80808080u, hi ^ 0x80808080u};
 }
 
+// ------------------------------------------------------------ split-K sums --
+// The sum over splits 0 .. splits-1 of the value at p + split * stride
+// (float or f32x4), added in split order starting from zero, as a loop of
+// one load and one add per split would; the loads are issued eight at a time
+// (past the last split, split s0's value is loaded again and not added), so
+// that a thread waits for memory once per eight splits instead of per split.
+template <typename V>
+__device__ __forceinline__ V sum_splits(const float *p, int splits, int64_t stride) {
+  V t = {};
+  for (int s0 = 0; s0 < splits; s0 += 8) {
+    V q[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      q[u] = *(const V *)(p + (int64_t)(s0 + u < splits ? s0 + u : s0) * stride);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (s0 + u < splits) t += q[u];
+  }
+  return t;
+}
+
 // ------------------------------------------------------------ device math --
 // x as an fp32 value in a register: the compiler may otherwise fuse the fma
 // that produced it with a following conversion to fp16 (v_fma_mix*_f16,

@@ -1062,8 +1062,7 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ w
   const int64_t step = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += step) {
     const int64_t m = i / N, n = i % N;
-    float v = 0.f;
-    for (int sp = 0; sp < splits; ++sp) v += ws[sp * stride + i];
+    float v = sum_splits<float>(ws + i, splits, stride);
     v = epilogue<EPI>(v, EPI != ZK_EPI_NONE ? to_f(bias[n]) : 0.f);
     if (EPI == ZK_EPI_BIAS_RESIDUAL) v += to_f(res[m * ldr + n]);
     C[m * ldc + n] = (OutT)as_f32(v);  // rounded to fp32, then to OutT, as the GEMM epilogue
@@ -1084,8 +1083,7 @@ __global__ __launch_bounds__(256) void splitk_reduce4(const float *__restrict__ 
   const int64_t step = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += step) {
     const int64_t e = 4 * i, m = e / N, n = e % N;
-    f32x4 v = {0.f, 0.f, 0.f, 0.f};
-    for (int sp = 0; sp < splits; ++sp) v += *(const f32x4 *)(ws + sp * stride + e);
+    f32x4 v = sum_splits<f32x4>(ws + e, splits, stride);
     OutT4 b4 = {}, r4 = {}, o4;
     if (EPI != ZK_EPI_NONE) b4 = *(const OutT4 *)(bias + n);
     if (EPI == ZK_EPI_BIAS_RESIDUAL) r4 = *(const OutT4 *)(res + m * ldr + n);

@@ -81,11 +81,12 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
     // the row's values from the partials, four columns per thread
     const float *pp = pin.ws + row * hidden;
     for (int c = threadIdx.x; c < hidden / 4; c += kLnWaves * kWave) {
-      f32x4 t = {0.f, 0.f, 0.f, 0.f};
-      for (int sp = 0; sp < pin.splits; ++sp) t += *(const f32x4 *)(pp + sp * pin.stride + 4 * c);
-      f16 *dst = reinterpret_cast<f16 *>(prow) + 4 * c;
+      const f16x4 bias = *(const f16x4 *)(pin.bias + 4 * c);
+      const f32x4 t = sum_splits<f32x4>(pp + 4 * c, pin.splits, pin.stride);
+      f16x4 o;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) dst[j] = (T)(t[j] + (float)pin.bias[4 * c + j]);
+      for (int j = 0; j < 4; ++j) o[j] = (T)as_f32(t[j] + (float)bias[j]);
+      *(f16x4 *)(reinterpret_cast<f16 *>(prow) + 4 * c) = o;
     }
     __syncthreads();
     if (threadIdx.x >= kWave) return;
@@ -97,8 +98,9 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
 
   const V *gv = reinterpret_cast<const V *>(gamma);
   const V *bv = reinterpret_cast<const V *>(beta);
-  // BATCH (rows read from memory, launches of at most kLnBatchWaves
-  // wavefronts): loads are issued ahead of their use, each from a valid
+  // BATCHED (rows read from memory by launches of at most kLnBatchWaves
+  // wavefronts, or formed in LDS): loads are issued ahead of their use, each
+  // from a valid
   // address (row 0, vector 0 where the lane has nothing to read): the row's
   // vectors (and residual) four at a time, and, for rows of at most four
   // vectors per lane, the output's gamma / beta (and post residual) at the
@@ -108,7 +110,8 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
   // rounds the other wavefronts hide it, and one load at a time per
   // wavefront was faster ([16384, 768] 13.9 us against 14.8 us batched).
   constexpr int CH = MAXV < 4 ? MAXV : 4;
-  constexpr bool PRE_OUT = BATCH && MAXV <= 4;
+  constexpr bool BATCHED = (PART == 0 && BATCH) || PART == 2;  // PART 2: row in LDS
+  constexpr bool PRE_OUT = BATCHED && MAXV <= 4;
   V go[PRE_OUT ? MAXV : 1], bo[PRE_OUT ? MAXV : 1], ro[PRE_OUT && RES == kResPost ? MAXV : 1];
   if constexpr (PRE_OUT) {
 #pragma unroll
@@ -131,7 +134,7 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
         f[j] += fmaf(((float)r[j] - rms.x) * rms.y, (float)rg[j], (float)rb[j]);
     }
   };
-  if constexpr (PART == 0 && BATCH) {
+  if constexpr (BATCHED) {
     // Branch-free: a lane with no vector k combines what it loaded from vector
     // 0 and keeps zeros (adding 0 leaves the sum as it is).
 #pragma unroll
@@ -140,7 +143,8 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
         const int idx = sub + (k0 + c) * LPR, ci = live && idx < nvec ? idx : 0;
-        xa[c] = xr[ci];
+        if constexpr (PART == 2) xa[c] = prow[ci];
+        else xa[c] = xr[ci];
         if constexpr (PRE) xq[c] = rr[ci];
         if constexpr (RES == kResPreLn) {
           xg[c] = reinterpret_cast<const V *>(rl.g)[ci];
@@ -168,24 +172,17 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
         V a;
         if constexpr (PART == 0) {
           a = xr[idx];
-        } else if constexpr (PART == 2) {
-          a = prow[idx];
         } else {
           static_assert(W == 8, "partials are summed 8 columns at a time");
           const float *pp = pin.ws + (row * hidden + (int64_t)idx * W);
-          float t[W] = {};
-          for (int sp = 0; sp < pin.splits; ++sp) {
-            const f32x4 lo = *(const f32x4 *)(pp + sp * pin.stride);
-            const f32x4 hi = *(const f32x4 *)(pp + sp * pin.stride + 4);
+          const f32x4 lo = sum_splits<f32x4>(pp, pin.splits, pin.stride);
+          const f32x4 hi = sum_splits<f32x4>(pp + 4, pin.splits, pin.stride);
+          const V bias = reinterpret_cast<const V *>(pin.bias)[idx];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              t[j] += lo[j];
-              t[j + 4] += hi[j];
-            }
+          for (int j = 0; j < 4; ++j) {
+            a[j] = (T)as_f32(lo[j] + (float)bias[j]);
+            a[j + 4] = (T)as_f32(hi[j] + (float)bias[j + 4]);
           }
-          const V bv = reinterpret_cast<const V *>(pin.bias)[idx];
-#pragma unroll
-          for (int j = 0; j < W; ++j) a[j] = (T)(t[j] + (float)bv[j]);
         }
         V r, rg, rb;
         if constexpr (PRE) r = rr[idx];
