@@ -328,6 +328,9 @@ void gemm_mfma_kernel(GemmParams p) {
   // does not count them holds until these loads return.)
   constexpr bool LN_ROWS = EPI == kEpiLnIn || EPI == kEpiLnInGelu || EPI == kEpiQkvAttn;
   static_assert(BM <= 64 * WM * WN, "one thread per tile row");
+  // Stands in for an absent operand (no statistics, no bias, no lengths) in
+  // the unconditional loads below; their values then go unused.
+  const void *any = p.A;
   float2 ln_pr[LN_ROWS ? kLnMaxParts : 1];
   if constexpr (LN_ROWS) {
     const bool mine = p.ln_part && (int)threadIdx.x < BM && m0 + (int)threadIdx.x < p.M;
@@ -343,25 +346,52 @@ void gemm_mfma_kernel(GemmParams p) {
   // MFMA.
   constexpr bool LN_COLS = EPI == kEpiLnIn || EPI == kEpiLnInGelu;
   typedef typename std::conditional<std::is_same<OutT, int8_t>::value, f16, OutT>::type BiasT;
-  float col_s[TN], col_c[TN];
+  // The raw values are loaded here, unconditionally (column 0 for columns
+  // past N), and col_s / col_c formed from them after the main loop: a load
+  // under a per-lane condition whose value is converted at once made the
+  // wavefront wait for it before requesting its first slice (three to six
+  // dependent loads in a row in the bias and dequantisation epilogues:
+  // int8 FFN-down + statistics 19.0 -> 18.6 us, encoders 0.8-1.7% faster).
+  BiasT col_bias[TN];
+  float col_x[TN], col_y[TN];
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
-    const int col = n0 + wn * WTN + j * MS + lane % MS;
-    col_s[j] = 1.f;
-    col_c[j] = 0.f;
+    const int col = n0 + wn * WTN + j * MS + lane % MS, cc = col < p.N ? col : 0;
     if constexpr (EPI == kEpiQkvAttn) {  // N is a whole number of 192-column tiles
-      const bool ln = p.ln_part != nullptr;
-      col_s[j] = ln ? p.ln_s[col] : 0.f;
-      col_c[j] = ln ? p.ln_c[col] : to_f(((const f16 *)p.bias)[col]);
-    } else if (col < p.N) {
-      if (EPI != ZK_EPI_NONE && !LN_COLS) col_c[j] = to_f(((const BiasT *)p.bias)[col]);
-      if (DEQ) col_s[j] = p.s_x * p.s_w[col];
-      if (LN_COLS) {
-        col_s[j] = p.ln_s[col];
-        col_c[j] = p.ln_c[col];
+      const bool ln = p.ln_part != nullptr, bias = p.bias != nullptr;
+      col_x[j] = (ln ? p.ln_s : (const float *)any)[ln ? cc : 0];
+      col_y[j] = (ln ? p.ln_c : (const float *)any)[ln ? cc : 0];
+      col_bias[j] = (bias ? (const BiasT *)p.bias : (const BiasT *)any)[bias ? cc : 0];
+    } else {
+      if constexpr (EPI != ZK_EPI_NONE && !LN_COLS) col_bias[j] = ((const BiasT *)p.bias)[cc];
+      if constexpr (DEQ) col_x[j] = p.s_w[cc];
+      if constexpr (LN_COLS) {
+        col_x[j] = p.ln_s[cc];
+        col_y[j] = p.ln_c[cc];
       }
     }
   }
+  float col_s[TN], col_c[TN];
+  auto form_cols = [&]() {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = n0 + wn * WTN + j * MS + lane % MS;
+      col_s[j] = 1.f;
+      col_c[j] = 0.f;
+      if constexpr (EPI == kEpiQkvAttn) {
+        const bool ln = p.ln_part != nullptr;
+        col_s[j] = ln ? col_x[j] : 0.f;
+        col_c[j] = ln ? col_y[j] : to_f(col_bias[j]);
+      } else if (col < p.N) {
+        if constexpr (EPI != ZK_EPI_NONE && !LN_COLS) col_c[j] = to_f(col_bias[j]);
+        if constexpr (DEQ) col_s[j] = p.s_x * col_x[j];
+        if constexpr (LN_COLS) {
+          col_s[j] = col_x[j];
+          col_c[j] = col_y[j];
+        }
+      }
+    }
+  };
   // kEpiResStats: the residual rows of the wave's first stripe (and their
   // LayerNorm statistics) are loaded into registers under the main loop,
   // issued right after the first slices; those of its other stripes right
@@ -415,7 +445,8 @@ void gemm_mfma_kernel(GemmParams p) {
   int attn_len = 0;
   if constexpr (EPI == kEpiQkvAttn) {
     const int b = m0 / p.seq + wave * 32 / p.seq;
-    attn_len = p.valid_lens && b < p.batch ? p.valid_lens[b] : p.seq;
+    const bool vl = p.valid_lens != nullptr;
+    attn_len = (vl ? p.valid_lens : (const int32_t *)any)[vl && b < p.batch ? b : 0];
   }
   const int kbytes = p.K * OP::kElem;
   const int64_t lda_b = p.lda * OP::kElem, ldb_b = p.ldb * OP::kElem;
@@ -560,6 +591,7 @@ void gemm_mfma_kernel(GemmParams p) {
     if (!EARLY_GB && p.res_ln) load_gb();
   }
   __syncthreads();  // every wave is done reading the ring; it becomes epilogue space
+  form_cols();
   if constexpr (EPI == kEpiQkvAttn) {
     // The tile is the Q, K and V columns of head tn (weights interleaved
     // per head: q, k, v, 64 rows each) for the 256 rows of the sequences
@@ -617,7 +649,10 @@ void gemm_mfma_kernel(GemmParams p) {
     const int sq = wave * 32 / p.seq;
     const int b = m0 / p.seq + sq;
     if (b < p.batch) {
-      int L = attn_len;
+      // opaque until here, so that the select below is not formed (and
+      // waited for) right after the load at kernel start
+      asm volatile("" : "+v"(attn_len));
+      int L = p.valid_lens ? attn_len : p.seq;
       L = L < 0 ? 0 : (L > p.seq ? p.seq : L);
       f16x8 qf[HD / 16];
 #pragma unroll
