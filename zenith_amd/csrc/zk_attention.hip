@@ -365,9 +365,10 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_q16_kernel(AttnParams p) {
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
         tmax = smax(smax(tmax, s4[kb][0]), smax(s4[kb][1], smax(s4[kb][2], s4[kb][3])));
-      tmax = smax(tmax, __shfl_xor(tmax, 16, 64));
+      const auto smax_op = [](float a, float b) { return smax(a, b); };
+      tmax = bfly<16>(tmax, smax_op);
       // finite unless MASK (without a mask, key t*KT < L is valid)
-      tmax = smax(tmax, __shfl_xor(tmax, 32, 64)) * p.scale_log2;
+      tmax = bfly<32>(tmax, smax_op) * p.scale_log2;
       if (__builtin_amdgcn_ballot_w64(tmax > m + 8.0f) != 0) {
         const float m_new = fmaxf(m, tmax);
         const float alpha = MASK && m_new == -__builtin_inff() ? 1.0f
@@ -390,8 +391,8 @@ __global__ __launch_bounds__(NW * 64) void fa_fwd_f16_q16_kernel(AttnParams p) {
           psum += e;
           pf[kb >> 1][4 * (kb & 1) + r] = (f16)e;
         }
-      psum += __shfl_xor(psum, 16, 64);
-      psum += __shfl_xor(psum, 32, 64);
+      psum = bfly<16>(psum, OpAdd{});
+      psum = bfly<32>(psum, OpAdd{});
       l += psum;
 #pragma unroll
       for (int db = 0; db < 4; ++db)
@@ -464,8 +465,8 @@ __global__ __launch_bounds__(256) void fa_fwd_f32_kernel(AttnParams p) {
       float d = 0.f;
 #pragma unroll
       for (int i = 0; i < 32; ++i) d = fmaf(q[i], Ks[j][part * 32 + i], d);
-#pragma unroll
-      for (int o = 1; o < TPQ; o <<= 1) d += __shfl_xor(d, o, 64);
+      if constexpr (TPQ >= 2) d = bfly<1>(d, OpAdd{});  // lanes of a query: a quad
+      if constexpr (TPQ >= 4) d = bfly<2>(d, OpAdd{});
       const int key = t * KT + j;
       s[j] = key < L && (!mrow || mrow[key]) ? d * scale : -__builtin_inff();
       tmax = fmaxf(tmax, s[j]);

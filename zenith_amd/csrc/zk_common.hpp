@@ -200,17 +200,57 @@ __device__ __forceinline__ float gelu_tanh_fast(float x) {
   return fmaf(-x, __builtin_amdgcn_rcpf(1.0f + e), x);
 }
 
+// One butterfly step without the LDS: op(t, t of lane l ^ O), op commutative
+// (a sum or a max: the order of its operands does not change the result).
+// - O = 32, 16: v_permlane32_swap / v_permlane16_swap, whose two results hold
+//   the pair {t(l), t(l ^ O)} in one order or the other;
+// - O = 8, 4: a DPP rotation of each 16-lane row by O, which pairs lane l with
+//   l ^ O wherever t repeats with period 2 O along the row: always for 8, and
+//   for 4 once the step with offset 8 has been done;
+// - O = 2, 1: a DPP permutation within each group of four lanes (exact).
+template <int O, typename Op>
+__device__ __forceinline__ float bfly(float t, Op op) {
+  static_assert(O == 32 || O == 16 || O == 8 || O == 4 || O == 2 || O == 1, "butterfly offset");
+  if constexpr (O == 32 || O == 16) {
+    const unsigned u = __float_as_uint(t);
+    const auto r = O == 32 ? __builtin_amdgcn_permlane32_swap(u, u, false, false)
+                           : __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  } else {
+    // row_ror:O, or quad_perm [1, 0, 3, 2] (O = 1) / [2, 3, 0, 1] (O = 2)
+    constexpr int ctrl = O >= 4 ? 0x120 + O : (O == 1 ? 0xB1 : 0x4E);
+    const float q =
+        __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t), ctrl, 0xF, 0xF, false));
+    return op(t, q);
+  }
+}
+// t of lane l ^ 1 (a DPP quad permutation, exact)
+__device__ __forceinline__ float lane_xor1(float t) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t), 0xB1, 0xF, 0xF, false));
+}
+struct OpAdd {
+  __device__ float operator()(float a, float b) const { return a + b; }
+};
+struct OpMax {
+  __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+// op over the N lanes of each aligned group of N (N = 2, 4, 16, 32 or 64),
+// the same pairing and order as a loop of __shfl_xor from N / 2 down to 1
+template <int N, typename Op>
+__device__ __forceinline__ float group_reduce(float t, Op op) {
+  static_assert(N == 64 || N == 32 || N == 16 || N == 4 || N == 2, "group size");
+  if constexpr (N >= 64) t = bfly<32>(t, op);
+  if constexpr (N >= 32) t = bfly<16>(t, op);
+  if constexpr (N >= 16) t = bfly<8>(t, op);
+  if constexpr (N >= 8) t = bfly<4>(t, op);
+  if constexpr (N >= 4) t = bfly<2>(t, op);
+  if constexpr (N >= 2) t = bfly<1>(t, op);
+  return t;
+}
+
 // Butterfly sum / max across the 64 lanes of a wavefront.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return group_reduce<64>(v, OpAdd{}); }
+__device__ __forceinline__ float wave_max(float v) { return group_reduce<64>(v, OpMax{}); }
 
 // ------------------------------------------------------------ LDS DMA --
 // Buffer loads that write LDS directly (buffer_load ... lds) are counted by

@@ -886,7 +886,7 @@ void gemm_mfma_kernel(GemmParams p) {
               }
             }
           }
-          const float mo = __shfl_xor(mean, 1), m2o = __shfl_xor(m2, 1);
+          const float mo = lane_xor1(mean), m2o = lane_xor1(m2);
           if (ok && hf == 0) {
             const float d = mo - mean;
             ((float2 *)p.part_out)[(int64_t)row * (p.N / kLnSeg) + col0 / kLnSeg + sg] =

@@ -203,11 +203,7 @@ __global__ __launch_bounds__(kLnWaves * kWave) void ln_wave_kernel(
       }
     }
   }
-  auto group_sum = [](float t) {
-#pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) t += __shfl_xor(t, o, kWave);
-    return t;
-  };
+  auto group_sum = [](float t) { return group_reduce<LPR>(t, OpAdd{}); };
   const float inv_h = 1.0f / (float)hidden;
   const float mean = group_sum(sum) * inv_h;
   float sq = 0.f;
