@@ -217,12 +217,16 @@ def test_linear_fp32(dev):
     np.testing.assert_allclose(y.cpu().numpy(), ops.gelu_erf(ops.linear(x, w, b)), rtol=1e-4, atol=1e-5)
 
 
-@pytest.mark.parametrize("M,K,N", [(128, 3072, 768), (128, 768, 768), (37, 1000, 200), (128, 768, 3072)])
+@pytest.mark.parametrize("M,K,N", [(128, 3072, 768), (128, 768, 768), (37, 1000, 200), (128, 768, 3072),
+                                   (64, 4096, 64), (64, 1152, 64), (64, 2304, 64)])
 @pytest.mark.parametrize("act", [None, "gelu", "residual"])
 def test_linear_split_k(dev, M, K, N, act):
     """Small-M products take the split-K path (caller workspace, fp32
     partials, ordered reduction with the epilogue): fp16 and fp32, against
-    the float64 product, and bit-identical on repeated calls."""
+    the float64 product, and bit-identical on repeated calls. The reduction
+    reads its partials eight splits at a time: the last three shapes split
+    16 ways (two whole groups), 9 and 12 ways in fp16 and 12 and 15 in fp32
+    (a last group of 1 to 7)."""
     from zenith_amd import _lib as L
     from zenith_amd import zenith_cuda as zc
 

@@ -22,10 +22,14 @@ def _t(a, dev, dtype):
 
 
 @pytest.mark.parametrize("rows,hidden", [(1, 768), (128, 768), (4096, 768), (33, 1024),
-                                         (7, 100), (5, 3), (16, 8192), (3, 20000)])
+                                         (7, 100), (5, 3), (16, 8192), (3, 20000),
+                                         (8192, 768), (8200, 768)])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 @pytest.mark.parametrize("with_res", [False, True])
 def test_layernorm(dev, rows, hidden, dtype, with_res):
+    """Rows of 768 fp16 values go two to a wavefront: 8192 rows are the
+    largest launch that batches its loads (4096 wavefronts), 8200 the next
+    shape, which loads one vector at a time."""
     from zenith_amd import zenith_cuda as zc
 
     x = synthetic.normal((rows, hidden), tag=1) * 3 + 0.5
