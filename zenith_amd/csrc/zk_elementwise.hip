@@ -117,6 +117,9 @@ __global__ __launch_bounds__(kGeluBlock) void gelu_rows(const T *__restrict__ x,
 #pragma unroll
     for (int u = 0; u < R; ++u)
       if (r0 + u < rows) v[u] = __builtin_nontemporal_load(xv + (r0 + u) * ncv + cv);
+    // the bias is opaque until the rows are requested: converted before the
+    // loop, it was waited for before the first row load was issued
+    if (BIAS) asm volatile("" : "+v"(b));
 #pragma unroll
     for (int u = 0; u < R; ++u) {
       if (r0 + u < rows) {
