@@ -167,6 +167,46 @@ __device__ __forceinline__ float attn32_softmax_max(f32x16 (&s)[2], int t, int L
   return MASK && m == -__builtin_inff() ? 0.0f : -m;
 }
 
+// attn32_softmax_max without a mask and with the accumulator's rescale left
+// to the caller: when resc (wavefront-uniform) is set, m has moved and l has
+// been multiplied by alpha, and o must be multiplied by alpha before the
+// next P.V product adds to it (so a P.V product of the previous tile may
+// still run first, as it would have before this tile's rescale).
+__device__ __forceinline__ float attn32_max_defer(f32x16 (&s)[2], int t, int L, float scale_log2,
+                                                  int lane, float &m, float &l, float &alpha,
+                                                  bool &resc) {
+  constexpr int KT = 64;
+  const int h32 = lane >> 5;
+  if (t * KT + KT > L) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = t * KT + kb * 32 + 8 * (r >> 2) + 4 * h32 + (r & 3);
+        if (key >= L) s[kb][r] = -__builtin_inff();
+      }
+  }
+  float tmax = -__builtin_inff();
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) tmax = smax(tmax, s[kb][r]);
+  {
+    float a, b;
+    half_swap(tmax, a, b);
+    tmax = smax(a, b) * scale_log2;
+  }
+  resc = __builtin_amdgcn_ballot_w64(tmax > m + 8.0f) != 0;
+  alpha = 1.0f;
+  if (resc) {
+    const float m_new = fmaxf(m, tmax);
+    alpha = __builtin_amdgcn_exp2f(m - m_new);
+    m = m_new;
+    l *= alpha;
+  }
+  return -m;
+}
+
 template <int D>
 __device__ __forceinline__ void attn32_softmax_exp(const f32x16 (&s)[2], float scale_log2,
                                                    float mneg, float &l, f16x8 (&pf)[2][2]) {

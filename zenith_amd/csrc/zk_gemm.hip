@@ -671,29 +671,46 @@ void gemm_mfma_kernel(GemmParams p) {
       // arithmetic per tile as attn32_tile, in the same order).
       const int ntiles = (L + 63) / 64;
       if (ntiles > 0) {
+        // Both tiles are processed whatever the length (a wave-uniform branch
+        // would let the compiler hoist the exponentials above it and lose the
+        // interleaving): with 64-token sequences tile 1 is tile 0 again, and
+        // wherever L <= 64 every key of tile 1 lies at or past L, so its
+        // probabilities are 0 and m, l and o stay exactly as they were.
+        const int off1 = p.seq > 64 ? 64 * HD : 0;
         f32x16 s0[2], s1[2];
-        f16x8 pf[2][2];
+        f16x8 pf0[2][2], pf1[2][2];
         attn32_qk<HD, true, HD>(Kt, qf, lane, s0);
         const float mneg = attn32_softmax_max<HD, false>(s0, 0, L, p.scale_log2, nullptr,
                                                          nullptr, lane, o, m, l);
-        // The second tile's 8 K-fragment reads and 8 MFMAs, interleaved with
-        // the first tile's exponentials. They are issued whatever the
-        // length (a wave-uniform branch here would let the compiler hoist the
-        // exponentials above it); with 64-token sequences they recompute
-        // tile 0 into s1, which is not used.
-        attn32_qk<HD, true, HD>(Kt + (p.seq > 64 ? 64 * HD : 0), qf, lane, s1);
-        attn32_softmax_exp<HD>(s0, p.scale_log2, mneg, l, pf);
+        // tile 1's 8 K-fragment reads and 8 MFMAs among tile 0's exponentials
+        attn32_qk<HD, true, HD>(Kt + off1, qf, lane, s1);
+        attn32_softmax_exp<HD>(s0, p.scale_log2, mneg, l, pf0);
         __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // DS reads
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
           __builtin_amdgcn_sched_group_barrier(0x402, 8, 0);  // VALU incl. exp
         }
-        attn32_pv<HD, true, HD>(Vt, pf, lane, o);
-        if (ntiles > 1) {
-          attn32_softmax<HD, false>(s1, 1, L, p.scale_log2, nullptr, nullptr, lane, o, m, l, pf);
-          attn32_pv<HD, true, HD>(Vt + 64 * HD, pf, lane, o);
+        // tile 0's P.V (16 transposing reads, 8 MFMAs) among tile 1's
+        // exponentials; tile 1's rescale of o, if any, after it
+        float alpha;
+        bool resc;
+        const float mneg1 = attn32_max_defer(s1, 1, L, p.scale_log2, lane, m, l, alpha, resc);
+        attn32_softmax_exp<HD>(s1, p.scale_log2, mneg1, l, pf1);
+        attn32_pv<HD, true, HD>(Vt, pf0, lane, o);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS reads
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x402, 8, 0);  // VALU incl. exp
         }
+        if (resc) {
+#pragma unroll
+          for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+        }
+        attn32_pv<HD, true, HD>(Vt + off1, pf1, lane, o);
       }
       const int grow = m0 + qr;
       if (grow < p.M) {
