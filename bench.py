@@ -326,6 +326,50 @@ def kernel_cases(torch, dev):
                 (f", output rows of {2 * (N + pad)} bytes as in the encoder" if pad else "")
         return setup
 
+    def ffn_frag(M=4096, H=768, I=3072, pad=FFN_PAD):
+        """The encoder's FFN at b32 s128 with its intermediate in fragment
+        order: FFN-up on the folded LayerNorm + GELU writing it
+        (zk_gemm_f16_ln_frag), or FFN-down + residual LayerNorm + statistics
+        reading it (zk_gemm_f16_res_stats_frag, weight rows padded as in the
+        encoder)."""
+        def up():
+            a = torch.from_numpy(synthetic.normal((M, H), tag=1)).to(dev, f16)
+            w = torch.from_numpy(synthetic.uniform((I, H), tag=2)).to(dev, f16) * 0.05
+            part = torch.zeros((M, H // 96, 2), dtype=torch.float32, device=dev)
+            part[..., 1] = 96.0
+            sc = torch.zeros(I, dtype=torch.float32, device=dev)
+            cc = torch.zeros(I, dtype=torch.float32, device=dev)
+            c = torch.empty(-(-M // 32) * 32 * I, dtype=f16, device=dev)
+            mr = torch.empty((M, 2), dtype=torch.float32, device=dev)
+            keep = (a, w, part, sc, cc, c, mr)
+            args = (a.data_ptr(), w.data_ptr(), c.data_ptr(), M, I, H, H, H, part.data_ptr(),
+                    1e-12, sc.data_ptr(), cc.data_ptr(), mr.data_ptr())
+            return (lambda i: _rc(L, lib.zk_gemm_f16_ln_frag(*args, s())) and keep), \
+                2.0 * M * I * H, "TFLOP/s", "fp16", "mfma", \
+                f"M={M} K={H} N={I} on LayerNorm-ed rows (folded) + GELU, output in fragment order"
+
+        def down():
+            from zenith_amd.encoder import to_fragment_order
+            a = torch.from_numpy(synthetic.uniform((M, I), tag=1)).to(dev, f16)
+            af = to_fragment_order(a)
+            w = torch.zeros((H, I + pad), dtype=f16, device=dev)
+            w[:, :I] = torch.from_numpy(synthetic.uniform((H, I), tag=2)).to(dev, f16) * 0.05
+            b = torch.zeros(H, dtype=f16, device=dev)
+            r = torch.from_numpy(synthetic.normal((M, H), tag=3)).to(dev, f16)
+            c = torch.empty((M, H), dtype=f16, device=dev)
+            ms = torch.zeros((M, 2), dtype=torch.float32, device=dev)
+            ms[:, 1] = 1.0
+            g = torch.ones(H, dtype=f16, device=dev)
+            be = torch.zeros(H, dtype=f16, device=dev)
+            part = torch.empty((M, H // 96, 2), dtype=torch.float32, device=dev)
+            keep = (a, af, w, b, r, c, ms, g, be, part)
+            args = (af.data_ptr(), w.data_ptr(), c.data_ptr(), M, H, I, I + pad, H, b.data_ptr(),
+                    r.data_ptr(), H, ms.data_ptr(), g.data_ptr(), be.data_ptr(), part.data_ptr())
+            return (lambda i: _rc(L, lib.zk_gemm_f16_res_stats_frag(*args, s())) and keep), \
+                2.0 * M * H * I, "TFLOP/s", "fp16", "mfma", \
+                f"M={M} K={I} N={H} + residual LayerNorm + row statistics, A in fragment order"
+        return up, down
+
     def qkv_attn_ln(B=32, S=128, heads=12):
         """The encoder's fused QKV projection + attention with the previous
         layer's LayerNorm folded in (layers 2-12 at s128)."""
@@ -438,6 +482,10 @@ def kernel_cases(torch, dev):
         "out_proj_res_stats": res_stats(4096, 768, 768),
         "ffn_up_ln": gemm_ln(4096, 768, 3072, True, pad=FFN_PAD),
         "ffn_down_res_stats": res_stats(4096, 3072, 768, pad=FFN_PAD),
+        # the same two with the intermediate in fragment order, as the
+        # encoder runs them at b32 s128
+        "ffn_up_ln_frag": ffn_frag()[0],
+        "ffn_down_res_stats_frag": ffn_frag()[1],
         "attn_s512": attn(512),
         "int8_ffn_up": gemm_i8(4096, 768, 3072, L.ZK_EPI_BIAS_GELU_ERF, requant=True),
         "int8_ffn_down": gemm_i8(4096, 3072, 768, E),
@@ -479,7 +527,8 @@ ATTN_COMPUTED = {
 
 # kernels one step of the timed encoder (b32 s128) launches, per layer: the
 # roofline line names the longest of them
-STEP_KERNELS = ("qkv_attn_ln_s128", "out_proj_res_stats", "ffn_up_ln", "ffn_down_res_stats")
+STEP_KERNELS = ("qkv_attn_ln_s128", "out_proj_res_stats", "ffn_up_ln_frag",
+                "ffn_down_res_stats_frag")
 KERNEL_DESC = {
     "gemm_qkv": "gemm_mfma_kernel<F16Op, bias> M=4096 K=768 N=2304 (QKV)",
     "gemm_out_proj": "gemm_mfma_kernel<F16Op, bias> M=4096 K=768 N=768 (out-projection)",
@@ -495,6 +544,10 @@ KERNEL_DESC = {
     "ffn_up_ln": "gemm_mfma_kernel<F16Op, folded LayerNorm + erf-GELU> M=4096 K=768 N=3072 (FFN-up)",
     "ffn_down_res_stats": "gemm_mfma_kernel<F16Op, bias + LayerNorm-ed residual + row statistics> "
                           "M=4096 K=3072 N=768 (FFN-down)",
+    "ffn_up_ln_frag": "gemm_mfma_kernel<F16Op, folded LayerNorm + erf-GELU, fragment-ordered "
+                      "output> M=4096 K=768 N=3072 (FFN-up)",
+    "ffn_down_res_stats_frag": "gemm_mfma_kernel<F16Op, fragment-ordered A, bias + LayerNorm-ed "
+                               "residual + row statistics> M=4096 K=3072 N=768 (FFN-down)",
     "add_layernorm": "ln_wave_kernel fp16 [4096,768] with residual",
 }
 

@@ -238,6 +238,36 @@ int zk_gemm_f16_ln(const void *A, const void *W, void *C, int64_t M, int64_t N, 
                    const float *ln_s, const float *ln_c, float *ln_out, int epilogue,
                    void *stream);
 
+/* Fragment order: the layout of an fp16 matrix X [R][K] (K a multiple of 16)
+ * in which it feeds a 32x32x16 MFMA as the A operand straight from memory.
+ * For row block rb (rows 32 rb .. 32 rb + 31) and k-step ks (columns
+ * 16 ks .. 16 ks + 15), the 512 halves at element (rb * K / 16 + ks) * 512
+ * hold, for lane l = 0 .. 63, X[32 rb + l % 32][16 ks + 8 (l / 32) + e] at
+ * element 8 l + e (e = 0 .. 7). A fragment-ordered buffer holds whole row
+ * blocks: ceil(R / 32) * 32 rows.
+ *
+ * zk_gemm_f16_ln with ZK_EPI_BIAS_GELU_ERF, C written in fragment order
+ * (ceil(M/32) * 32 x N; rows past M are not written). N a multiple of 64.
+ * The values are zk_gemm_f16_ln's, bit for bit. No reference counterpart:
+ * the FFN intermediate between the two FFN GEMMs of the reference layer
+ * (benchmarks/bert_fp16_full.py:133-139) laid out for zk_gemm_f16_res_stats_frag. */
+int zk_gemm_f16_ln_frag(const void *A, const void *W, void *C, int64_t M, int64_t N, int64_t K,
+                        int64_t lda, int64_t ldw, const float *ln_part, float ln_eps,
+                        const float *ln_s, const float *ln_c, float *ln_out, void *stream);
+
+/* zk_gemm_f16_res_stats with A in fragment order (ceil(M/32) * 32 x K; rows
+ * past M are read and their products discarded). K a multiple of 64. Each
+ * 1 KB fragment reaches LDS with one contiguous DMA instruction and is read
+ * back linearly. Runs the 128x96 tile at every M; the values and statistics
+ * are zk_gemm_f16_res_stats's, bit for bit, wherever that takes the same
+ * tile (M < 10240 at N = 768). No reference counterpart (see
+ * zk_gemm_f16_ln_frag). */
+int zk_gemm_f16_res_stats_frag(const void *A, const void *W, void *C, int64_t M, int64_t N,
+                               int64_t K, int64_t ldw, int64_t ldc, const void *bias,
+                               const void *res, int64_t ldr, const float *res_ln,
+                               const void *res_gamma, const void *res_beta, float *part_out,
+                               void *stream);
+
 /* Flash-attention forward, non-causal, online softmax with fp32 statistics.
  *   O[b,h,s,:] = softmax(scale * Q[b,h,s,:] . K[b,h,:,:]^T) . V[b,h,:,:]
  * Tensors are addressed by strides (elements): strides[0..2] are the

@@ -1,0 +1,168 @@
+"""GPU parity: the FFN intermediate in fragment order.
+
+- zk_gemm_f16_res_stats_frag reads A in fragment order (each lane loads its
+  MFMA A fragments straight from memory) and must give zk_gemm_f16_res_stats's
+  output and statistics bit for bit, on the same rows in row-major order,
+  wherever both run the 128x96 tile; the padding rows of the
+  fragment-ordered A (past M) are filled with NaN, which must reach no stored
+  value. Where zk_gemm_f16_res_stats takes its 256x192 tile (M = 16384,
+  N = 768) the two launches' results are not bit-identical (the frag entry
+  always runs the 128x96 tile), and the frag result is checked against the
+  oracle at the fp16 bar instead, as is one other shape.
+- zk_gemm_f16_ln_frag writes zk_gemm_f16_ln's GELU output (bit for bit) in
+  fragment order, on every tile configuration it runs (256x256, 256x192,
+  128x128 and the 128x96 tile that replaces the 16x16-MFMA ones), and leaves
+  the padding rows past M untouched.
+- The folded encoder with and without the fragment-ordered FFN gives the same
+  output, bit for bit.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ops
+from tests.conftest import fp16_tol
+from zenith_amd import _lib as L
+from zenith_amd import synthetic
+from zenith_amd.encoder import (BertEncoder, fold_layernorm, from_fragment_order,
+                                to_fragment_order)
+
+pytestmark = pytest.mark.gpu
+
+SEG = 96
+EPS = 1e-12
+
+
+def _t(a, dev, dtype=torch.float16):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev, dtype)
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _res_stats(name, a_ptr, lda, tw, tb, tr, st, tg, tbe, M, N, K, dev):
+    c = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+    part = torch.full((M, N // SEG, 2), float("nan"), dtype=torch.float32, device=dev)
+    ln = st is not None
+    head = (a_ptr, tw.data_ptr(), c.data_ptr(), M, N, K) + ((lda,) if lda else ()) + (K, N)
+    L.call(name, *head, tb.data_ptr(), tr.data_ptr(), N, st.data_ptr() if ln else None,
+           tg.data_ptr() if ln else None, tbe.data_ptr() if ln else None, part.data_ptr(),
+           _stream())
+    torch.cuda.synchronize()
+    return c, part
+
+
+@pytest.mark.parametrize("M,K,N", [(4096, 3072, 768), (1000, 3072, 768), (4096, 768, 768),
+                                   (100, 64, 96), (300, 256, 288), (16384, 3072, 768)])
+@pytest.mark.parametrize("ln_res", [False, True])
+def test_res_stats_frag_matches_row_major(dev, M, K, N, ln_res):
+    a = synthetic.round_f16(synthetic.normal((M, K), tag=180))
+    w = synthetic.round_f16(synthetic.normal((N, K), tag=181, std=1.0 / math.sqrt(K)))
+    b = synthetic.round_f16(synthetic.normal((N,), tag=182, std=0.1))
+    res = synthetic.round_f16(synthetic.normal((M, N), tag=183))
+    g = synthetic.round_f16(1.0 + synthetic.normal((N,), tag=184, std=0.2))
+    be = synthetic.round_f16(synthetic.normal((N,), tag=185, std=0.2))
+    ta, tw, tb, tr, tg, tbe = (_t(v, dev) for v in (a, w, b, res, g, be))
+    st = None
+    if ln_res:
+        r64 = res.astype(np.float64)
+        st = _t(np.stack([r64.mean(1), 1.0 / np.sqrt(r64.var(1) + EPS)], -1), dev,
+                torch.float32)
+    af = to_fragment_order(ta)
+    Mp = -(-M // 32) * 32
+    if Mp > M:  # padding rows: read, never stored
+        af.view(Mp // 32, K // 16, 2, 32, 8)[-1, :, :, M % 32:, :] = float("nan")
+    print(f"zk_gemm_f16_res_stats_frag M={M} K={K} N={N} ln_res={ln_res}", flush=True)
+    c0, p0 = _res_stats("zk_gemm_f16_res_stats", ta.data_ptr(), K, tw, tb, tr, st, tg, tbe,
+                        M, N, K, dev)
+    c1, p1 = _res_stats("zk_gemm_f16_res_stats_frag", af.data_ptr(), 0, tw, tb, tr, st, tg,
+                        tbe, M, N, K, dev)
+    assert not torch.isnan(c1).any()
+    same_tile = not (M >= 1024 and N % 192 == 0 and -(-M // 256) * (N // 192) >= 160)
+    if same_tile:
+        assert torch.equal(c0.view(torch.int16), c1.view(torch.int16))
+        assert torch.equal(p0.view(torch.int32), p1.view(torch.int32))
+    if (M, K, N) == (1000, 3072, 768) or not same_tile:
+        r = res
+        if ln_res:
+            s = st.cpu().numpy()
+            r = (res - s[:, :1]) * s[:, 1:] * g + be
+        ok, worst = fp16_tol(c1.float().cpu().numpy(), ops.linear(a, w, b) + r)
+        assert ok, worst
+
+
+def _ln_frag_case(dev, M, K, N):
+    x = synthetic.round_f16(synthetic.normal((M, K), tag=190) * 1.5 + 0.3)
+    w = synthetic.round_f16(synthetic.normal((N, K), tag=191, std=1.0 / math.sqrt(K)))
+    b = synthetic.round_f16(synthetic.normal((N,), tag=192, std=0.1))
+    g = synthetic.round_f16(1.0 + synthetic.normal((K,), tag=193, std=0.2))
+    be = synthetic.round_f16(synthetic.normal((K,), tag=194, std=0.2))
+    wf, s, cc = fold_layernorm(w, b, g, be)
+    x64 = x.astype(np.float64).reshape(M, K // SEG, SEG)
+    mean = x64.mean(-1)
+    part = np.stack([mean, ((x64 - mean[..., None]) ** 2).sum(-1)], -1).astype(np.float32)
+    tx, twf = _t(x, dev), _t(wf, dev)
+    tp, ts, tc = (_t(v, dev, torch.float32) for v in (part, s, cc))
+    return tx, twf, tp, ts, tc
+
+
+@pytest.mark.parametrize("M,K,N", [(4096, 768, 3072), (16384, 768, 3072), (1000, 96, 10240),
+                                   (2048, 768, 3072), (100, 96, 128), (300, 288, 192)])
+def test_ln_frag_matches_row_major(dev, M, K, N):
+    tx, twf, tp, ts, tc = _ln_frag_case(dev, M, K, N)
+    out = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+    mr0 = torch.full((M, 2), float("nan"), dtype=torch.float32, device=dev)
+    mr1 = torch.full((M, 2), float("nan"), dtype=torch.float32, device=dev)
+    Mp = -(-M // 32) * 32
+    fr = torch.full((Mp * N,), 7.0, dtype=torch.float16, device=dev)
+    print(f"zk_gemm_f16_ln_frag M={M} K={K} N={N}", flush=True)
+    L.call("zk_gemm_f16_ln", tx.data_ptr(), twf.data_ptr(), out.data_ptr(), M, N, K, K, K, N,
+           tp.data_ptr(), EPS, ts.data_ptr(), tc.data_ptr(), mr0.data_ptr(),
+           L.ZK_EPI_BIAS_GELU_ERF, _stream())
+    L.call("zk_gemm_f16_ln_frag", tx.data_ptr(), twf.data_ptr(), fr.data_ptr(), M, N, K, K, K,
+           tp.data_ptr(), EPS, ts.data_ptr(), tc.data_ptr(), mr1.data_ptr(), _stream())
+    torch.cuda.synchronize()
+    y = from_fragment_order(fr, M, N)
+    assert torch.equal(y.view(torch.int16), out.view(torch.int16))
+    assert torch.equal(mr0.view(torch.int32), mr1.view(torch.int32))
+    if Mp > M:  # rows past M are not written
+        pad = fr.view(Mp // 32, N // 16, 2, 32, 8)[-1, :, :, M % 32:, :]
+        assert bool((pad == 7.0).all())
+
+
+def test_frag_shape_errors(dev):
+    t = torch.zeros(1 << 16, dtype=torch.float16, device=dev)
+    f = torch.zeros(1 << 12, dtype=torch.float32, device=dev)
+    p = t.data_ptr()
+    lib = L.load()
+    # K not a multiple of 64 (fragment-ordered A is read in 64-deep slices)
+    rc = lib.zk_gemm_f16_res_stats_frag(p, p, p, 32, 96, 96, 96, 96, p, p, 96, None, None, None,
+                                        f.data_ptr(), _stream())
+    assert rc == L.ZK_ERR_UNSUPPORTED, L.last_error()
+    # N not a multiple of 64 (the consumer's K)
+    rc = lib.zk_gemm_f16_ln_frag(p, p, p, 32, 96, 96, 96, 96, f.data_ptr(), EPS, f.data_ptr(),
+                                 f.data_ptr(), None, _stream())
+    assert rc == L.ZK_ERR_UNSUPPORTED, L.last_error()
+    torch.cuda.synchronize()
+
+
+def test_encoder_frag_ffn_bit_identical(dev):
+    layers = synthetic.bert_weights_wired(3, seed=7)
+    B, S = 32, 128
+    x = torch.from_numpy(synthetic.hidden_states(B, S, seed=7)).to(dev, torch.float16)
+    lens = torch.from_numpy(synthetic.padding_lengths(B, S)).to(dev)
+    outs = []
+    for frag in (True, False):
+        enc = BertEncoder(layers, device=dev)
+        enc.ffn_frag = frag
+        assert enc.frag_ffn(B * S) == frag
+        outs.append(enc.forward(x, lens).clone())
+        torch.cuda.synchronize()
+        if frag:
+            assert enc._bufs["u_frag"] is not None
+        del enc
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))

@@ -93,6 +93,15 @@ struct GemmParams {
   const void *res_gamma;
   const void *res_beta;
   float *part_out;
+  // Fragment order, the layout of an fp16 MFMA operand of 32 rows: for row
+  // block rb (rows 32 rb .. +31) and k-step ks (columns 16 ks .. +15) of an
+  // R x K matrix, the 1 KB at byte (rb * K / 16 + ks) * 1024 holds lane l's
+  // 16 bytes, X[32 rb + l % 32][16 ks + 8 (l / 32) .. +7], at byte 16 l.
+  // a_pk: A in fragment order (kernels instantiated with APK, K a multiple
+  // of 64; lda unused): each fragment is one 1 KB DMA into LDS.
+  // c_pk: C written in fragment order (kEpiLnInGelu; ldc unused).
+  const void *a_pk;
+  int c_pk;
 };
 
 // Internal epilogues (not public ZK_EPI_* values): the fused QKV projection +
@@ -297,7 +306,7 @@ constexpr int gemm_waves_per_eu(int smem_bytes, int nw) {
 }
 
 template <class OP, int BM, int BN, int MS, int BKB, int ST, int WM, int WN, int EPI, typename OutT,
-          bool DEQ>
+          bool DEQ, bool APK = false>
 __global__ __launch_bounds__(64 * WM * WN)
 __attribute__((amdgpu_waves_per_eu(gemm_waves_per_eu(GemmCfg<OP, BM, BN, MS, BKB, ST, WM, WN>::SMEM,
                                                      WM * WN))))
@@ -330,7 +339,7 @@ void gemm_mfma_kernel(GemmParams p) {
   static_assert(BM <= 64 * WM * WN, "one thread per tile row");
   // Stands in for an absent operand (no statistics, no bias, no lengths) in
   // the unconditional loads below; their values then go unused.
-  const void *any = p.A;
+  const void *any = APK ? p.a_pk : p.A;
   float2 ln_pr[LN_ROWS ? kLnMaxParts : 1];
   if constexpr (LN_ROWS) {
     const bool mine = p.ln_part && (int)threadIdx.x < BM && m0 + (int)threadIdx.x < p.M;
@@ -397,13 +406,10 @@ void gemm_mfma_kernel(GemmParams p) {
   // issued right after the first slices; those of its other stripes right
   // after the main loop, all at once, instead of one dependent load per
   // vector in the epilogue. Every lane loads (out-of-range lanes from the
-  // first element), so a stripe is exactly 2 NPV vector loads, which the
-  // slice waits that see them in flight count.
+  // first element), so a stripe is exactly 2 NPV vector loads.
   constexpr int NPV0 = (MS * (WTN / 8) + 63) / 64;
   constexpr bool RES_PREF = EPI == kEpiResStats && std::is_same<OutT, f16>::value && NPV0 <= 6;
   constexpr int NPV = RES_PREF ? NPV0 : 1, NPT = RES_PREF ? G::TM : 1;
-  // loads issued right after the prologue slices, per wave
-  constexpr int NXL = RES_PREF ? 2 * NPV : 0;
   f16x8 res_pv[NPT][NPV];
   float2 res_ms[NPT][NPV];
   auto load_res = [&](int i) {
@@ -451,9 +457,13 @@ void gemm_mfma_kernel(GemmParams p) {
   const int kbytes = p.K * OP::kElem;
   const int64_t lda_b = p.lda * OP::kElem, ldb_b = p.ldb * OP::kElem;
   const int a_rows = min(BM, p.M - m0), b_rows = min(BN, p.N - n0);
+  // APK: the tile's row blocks of the fragment-ordered A, (K / 16) KB each
+  const int a_blocks = min(BM / 32, (p.M + 31) / 32 - m0 / 32);
   const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)((const char *)p.A + (int64_t)m0 * lda_b), (short)0,
-      (int)((a_rows - 1) * lda_b + kbytes), 0x00020000);
+      APK ? (void *)((const char *)p.a_pk + (int64_t)(m0 / 32) * (p.K / 16) * 1024)
+          : (void *)((const char *)p.A + (int64_t)m0 * lda_b),
+      (short)0, APK ? a_blocks * (p.K / 16) * 1024 : (int)((a_rows - 1) * lda_b + kbytes),
+      0x00020000);
   const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
       (void *)((const char *)p.B + (int64_t)n0 * ldb_b), (short)0,
       (int)((b_rows - 1) * ldb_b + kbytes), 0x00020000);
@@ -462,13 +472,22 @@ void gemm_mfma_kernel(GemmParams p) {
   // [(wave * I + g) * RPI, +RPI); lane l lands at LDS slot l % CH of row
   // (l / CH) of that group and therefore fetches the logical chunk whose
   // swizzled slot that is.
+  // APK: instruction g moves fragment f = wave * IA + g of the slice (row
+  // block f / KS, k-step f % KS), 1 KB contiguous, to LDS byte f * 1024 of
+  // the stage's A part, where lane l reads its 16 bytes of it back.
   int offA[IA], chA[IA], offB[IB], chB[IB];
 #pragma unroll
   for (int g = 0; g < IA; ++g) {
-    const int row = (wave * IA + g) * G::RPI + lane / CH;
-    const int c = lds_slot<BKB>(row, lane % CH);  // the swizzle is an involution
-    chA[g] = c * 16;
-    offA[g] = (int)(row * lda_b) + c * 16;
+    if constexpr (APK) {
+      const int f = wave * IA + g;
+      chA[g] = 0;
+      offA[g] = ((f / KS) * (p.K / 16) + f % KS) * 1024 + lane * 16;
+    } else {
+      const int row = (wave * IA + g) * G::RPI + lane / CH;
+      const int c = lds_slot<BKB>(row, lane % CH);  // the swizzle is an involution
+      chA[g] = c * 16;
+      offA[g] = (int)(row * lda_b) + c * 16;
+    }
   }
 #pragma unroll
   for (int g = 0; g < IB; ++g) {
@@ -492,14 +511,20 @@ void gemm_mfma_kernel(GemmParams p) {
   // buffer ks & 1 (KS is even), so the first k-step of the next slice can
   // be read while the last one of this slice is multiplied.
   Frag fa[2][TM], fb[2][TN];
+  static_assert(!APK || (MS == 32 && std::is_same<OP, F16Op>::value), "fragment-ordered A");
+  constexpr int PER = IA + IB;  // DMA instructions per slice and wave
   auto rd = [&](int stage, int ks, int buf) {
     const char *As = smem + stage * G::STAGE;
     const char *Bs = As + BM * BKB;
     const int c = ks * KCH + fch;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      const int row = wm * WTM + i * MS + frow;
-      fa[buf][i] = *(const Frag *)(As + row * BKB + lds_slot<BKB>(row, c) * 16);
+      if constexpr (APK) {
+        fa[buf][i] = *(const Frag *)(As + (((wm * WTM + i * MS) / 32) * KS + ks) * 1024 + lane * 16);
+      } else {
+        const int row = wm * WTM + i * MS + frow;
+        fa[buf][i] = *(const Frag *)(As + row * BKB + lds_slot<BKB>(row, c) * 16);
+      }
     }
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
@@ -530,7 +555,9 @@ void gemm_mfma_kernel(GemmParams p) {
     _Pragma("unroll") for (int g = 0; g < IA; ++g)                                            \
         __builtin_amdgcn_raw_ptr_buffer_load_lds(                                             \
             rA, ZK_LDS(as_ + (wave * IA + g) * 1024), 16,                                     \
-            kb_ + chA[g] < kbytes ? offA[g] + kb_ : 0x7ffffff0, 0, 0, 0);                     \
+            kb_ + chA[g] < kbytes ? offA[g] + (APK ? kb_ / BKB * KS * 1024 : kb_)            \
+                                  : 0x7ffffff0,                                               \
+            0, 0, 0);                                                                         \
     _Pragma("unroll") for (int g = 0; g < IB; ++g)                                            \
         __builtin_amdgcn_raw_ptr_buffer_load_lds(                                             \
             rB, ZK_LDS(bs_ + (wave * IB + g) * 1024), 16,                                     \
@@ -539,20 +566,27 @@ void gemm_mfma_kernel(GemmParams p) {
 #else
 #define ZK_ISSUE(kt, stage) ((void)(kt), (void)(stage))
 #endif
+  // res_first: the first stripe's residual rows are requested before the
+  // first slice. Loads into registers and DMA loads into LDS complete in
+  // order only among their own kind, so a slice wait (at most c loads in
+  // flight) guarantees a slice only through the c DMA loads issued after
+  // it, and holds for any load into registers still in flight. Issued after
+  // the first slices, these loads made the first waits hold until they
+  // returned (fp16 encoder 1.6% slower); allowed for as younger loads in
+  // those waits, they could have let a wave read a slice before it landed
+  // (as loads of A into registers beside the W DMA were seen to do).
+  if constexpr (RES_PREF) {
+    load_res(0);
+    asm volatile("" ::: "memory");
+  }
   {
     // Prologue: one slice per stage.
 #pragma unroll
     for (int s = 0; s < ST; ++s)
       if (s < nk) ZK_ISSUE(s, s);
-    // the residual loads follow the prologue slices (the empty asm keeps
-    // the compiler from moving them ahead): the waits for slices 0 .. ST - 1
-    // let these NXL younger loads stay in flight
-    if constexpr (RES_PREF) {
-      asm volatile("" ::: "memory");
-      load_res(0);
-      asm volatile("" ::: "memory");
-    }
-    wait_slices<ST - 1, IA + IB, NXL>(nk - 1);
+    // (the residual rows, loaded into registers before the prologue, are
+    // not counted by the slice waits: see res_first)
+    wait_slices<ST - 1, PER>(nk - 1);
     lds_barrier();
     rd(0, 0, 0);
     // Main loop over slices. Before the last k-step of slice kt every wave
@@ -572,8 +606,7 @@ void gemm_mfma_kernel(GemmParams p) {
     for (int kt = 0; kt + 1 < nk; ++kt) {
       steps_but_last(stage);
       const int next = stage + 1 == ST ? 0 : stage + 1;
-      if (NXL > 0 && kt + 1 < ST) wait_slices<ST - 2, IA + IB, NXL>(nk - 2 - kt);
-      else wait_slices<ST - 2, IA + IB>(nk - 2 - kt);
+      wait_slices<ST - 2, PER>(nk - 2 - kt);
       lds_barrier();
       if (kt + ST < nk) ZK_ISSUE(kt + ST, stage);
       rd(next, 0, 0);
@@ -768,6 +801,10 @@ void gemm_mfma_kernel(GemmParams p) {
       return r;
     };
     constexpr int VPR = WTN / 8;  // 8-column vectors per stripe row
+    // fragment-ordered output (p.c_pk): the folded-LayerNorm GELU epilogue of
+    // the fp16 32x32 tiles (FFN-up, whose output is FFN-down's A)
+    constexpr bool CPK = EPI == kEpiLnInGelu && MS == 32 && std::is_same<OutT, f16>::value &&
+                         WTN % 16 == 0;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       // LN_IN: (mean, rstd) of the rows this lane's registers hold
@@ -864,6 +901,31 @@ void gemm_mfma_kernel(GemmParams p) {
           }
         }
       };
+      if constexpr (CPK) {
+        if (p.c_pk) {
+          // C in fragment order: the stripe (32 rows, a whole row block) is
+          // WTN / 16 k-steps of the consumer's A, each 1 KB contiguous; lane l
+          // stores row l % 32, columns 8 (l / 32) .. +7 of the k-step
+          const int rl = lane & 31;
+          const int64_t blk = (int64_t)(row0 / 32) * (p.N / 16) + col0 / 16;
+#pragma unroll
+          for (int kc = 0; kc < WTN / 16; ++kc) {
+            const int cl = kc * 16 + (lane >> 5) * 8;
+            if (row0 + rl < p.M && col0 + cl < p.N) {
+              const float *src = ws + rl * G::EPITCH + cl;
+              const f32x4 lo = *(const f32x4 *)src, hi = *(const f32x4 *)(src + 4);
+              f16x8 h;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                h[e] = (f16)lo[e];
+                h[e + 4] = (f16)hi[e];
+              }
+              store_nt((f16x8 *)((f16 *)p.C + ((blk + kc) * 64 + lane) * 8), h);
+            }
+          }
+          continue;
+        }
+      }
       if constexpr (RES_PREF) {
 #pragma unroll
         for (int k = 0; k < NPV; ++k)
@@ -931,9 +993,8 @@ constexpr int kNumCfgs = 6;
 // Returns false when no kernel of this configuration implements `epi` for
 // these operand types (nothing is launched then): callers turn that into
 // ZK_ERR_UNSUPPORTED instead of leaving the output unwritten.
-template <class OP, int BM, int BN, int MS, int BKB, int ST, typename OutT, bool DEQ, int WM = 2,
-          int WN = 2>
-static bool launch_epi(GemmParams p, int epi, hipStream_t s) {
+// Sets p's tile counts and XCD grouping for BM x BN tiles; returns the grid.
+static int tile_grid(GemmParams &p, int BM, int BN) {
   p.tiles_n = (p.N + BN - 1) / BN;
   p.tiles_m = (p.M + BM - 1) / BM;
   const int grid = p.tiles_m * p.tiles_n * (p.splits > 1 ? p.splits : 1);
@@ -943,6 +1004,13 @@ static bool launch_epi(GemmParams p, int epi, hipStream_t s) {
   const int per_xcd = (grid + 7) / 8;
   while (gm * 2 <= p.tiles_m && gm * gm * 4 <= per_xcd) gm *= 2;
   p.group_m = gm;
+  return grid;
+}
+
+template <class OP, int BM, int BN, int MS, int BKB, int ST, typename OutT, bool DEQ, int WM = 2,
+          int WN = 2>
+static bool launch_epi(GemmParams p, int epi, hipStream_t s) {
+  const int grid = tile_grid(p, BM, BN);
 #define ZK_L(E) \
   (gemm_mfma_kernel<OP, BM, BN, MS, BKB, ST, WM, WN, E, OutT, DEQ><<<grid, 64 * WM * WN, 0, s>>>(p), \
    true)
@@ -971,6 +1039,15 @@ static bool launch_epi(GemmParams p, int epi, hipStream_t s) {
       return false;
   }
 #undef ZK_L
+}
+
+// The residual + statistics epilogue on fragment-ordered A (p.a_pk): the
+// fp16 128x96 tile of 4 x 1 waves and 3-stage ring that FFN-down runs on
+// with row-major A.
+static void launch_frag_res_stats(GemmParams p, hipStream_t s) {
+  const int grid = tile_grid(p, 128, 96);
+  gemm_mfma_kernel<F16Op, 128, 96, 32, 128, 3, 4, 1, kEpiResStats, f16, false, true>
+      <<<grid, 256, 0, s>>>(p);
 }
 
 // Shape -> configuration, from measurements at the BERT shapes (M = 4096)
@@ -1514,6 +1591,13 @@ static int res_stats_run(const char *who, GemmParams p, const float *res_ln, con
   p.res_gamma = res_gamma;
   p.res_beta = res_beta;
   p.part_out = part_out;
+  if (p.a_pk) {
+    if constexpr (std::is_same<OP, F16Op>::value && !DEQ) {
+      launch_frag_res_stats(p, as_stream(stream));
+      return launched(true, who, kEpiResStats);
+    }
+    return fail(ZK_ERR_UNSUPPORTED, "%s: fragment-ordered A is fp16 only", who);
+  }
   const int64_t t192 = (M + 255) / 256 * (N / 192);
   const bool ok = launch_mfma<OP, f16, DEQ>(p, kEpiResStats, as_stream(stream),
                                             M >= 1024 && N % 192 == 0 && t192 >= 160 ? 5 : 4);
@@ -1533,6 +1617,21 @@ extern "C" int zk_gemm_f16_res_stats(const void *A, const void *W, void *C, int6
   return res_stats_run<F16Op, false>(who, p, res_ln, res_gamma, res_beta, part_out, stream);
 }
 
+extern "C" int zk_gemm_f16_res_stats_frag(const void *A, const void *W, void *C, int64_t M,
+                                          int64_t N, int64_t K, int64_t ldw, int64_t ldc,
+                                          const void *bias, const void *res, int64_t ldr,
+                                          const float *res_ln, const void *res_gamma,
+                                          const void *res_beta, float *part_out, void *stream) {
+  const char *who = "zk_gemm_f16_res_stats_frag";
+  int st = check_ln_gemm(who, A, W, C, M, N, K, K, ldw, ldc);
+  if (st) return st;
+  if (M == 0 || N == 0) return ZK_OK;
+  if (K % 64) return fail(ZK_ERR_UNSUPPORTED, "%s: K must be a multiple of 64", who);
+  GemmParams p{A, W, C, (int)M, (int)N, (int)K, K, ldw, ldc, bias, res, ldr, 1.f, nullptr, 0};
+  p.a_pk = A;
+  return res_stats_run<F16Op, false>(who, p, res_ln, res_gamma, res_beta, part_out, stream);
+}
+
 extern "C" int zk_gemm_i8_res_stats(const int8_t *A, const int8_t *W, void *C, int64_t M,
                                     int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc,
                                     float s_x, const float *s_w, const void *bias,
@@ -1549,11 +1648,10 @@ extern "C" int zk_gemm_i8_res_stats(const int8_t *A, const int8_t *W, void *C, i
   return res_stats_run<I8Op, true>(who, p, res_ln, res_gamma, res_beta, part_out, stream);
 }
 
-extern "C" int zk_gemm_f16_ln(const void *A, const void *W, void *C, int64_t M, int64_t N,
-                              int64_t K, int64_t lda, int64_t ldw, int64_t ldc,
-                              const float *ln_part, float ln_eps, const float *ln_s,
-                              const float *ln_c, float *ln_out, int epilogue, void *stream) {
-  const char *who = "zk_gemm_f16_ln";
+static int gemm_f16_ln(const char *who, const void *A, const void *W, void *C, int64_t M,
+                       int64_t N, int64_t K, int64_t lda, int64_t ldw, int64_t ldc,
+                       const float *ln_part, float ln_eps, const float *ln_s, const float *ln_c,
+                       float *ln_out, int epilogue, bool frag, void *stream) {
   int st = check_ln_gemm(who, A, W, C, M, N, K, lda, ldw, ldc);
   if (st) return st;
   if (M == 0 || N == 0) return ZK_OK;
@@ -1575,7 +1673,32 @@ extern "C" int zk_gemm_f16_ln(const void *A, const void *W, void *C, int64_t M, 
   p.ln_c = ln_c;
   p.ln_out = ln_out;
   const int epi = epilogue == ZK_EPI_BIAS ? kEpiLnIn : kEpiLnInGelu;
-  return launched(launch_mfma<F16Op, f16, false>(p, epi, as_stream(stream)), who, epi);
+  int cfg = pick_cfg(p.M, p.N, p.K);
+  if (frag) {
+    // every 32x32-MFMA tile (0, 1, 4, 5) has the fragment-ordered store; the
+    // 16x16 ones (2, 3) give way to the 128x96 tile
+    p.c_pk = 1;
+    if (cfg == 2 || cfg == 3) cfg = 4;
+  }
+  return launched(launch_mfma<F16Op, f16, false>(p, epi, as_stream(stream), cfg), who, epi);
+}
+
+extern "C" int zk_gemm_f16_ln(const void *A, const void *W, void *C, int64_t M, int64_t N,
+                              int64_t K, int64_t lda, int64_t ldw, int64_t ldc,
+                              const float *ln_part, float ln_eps, const float *ln_s,
+                              const float *ln_c, float *ln_out, int epilogue, void *stream) {
+  return gemm_f16_ln("zk_gemm_f16_ln", A, W, C, M, N, K, lda, ldw, ldc, ln_part, ln_eps, ln_s,
+                     ln_c, ln_out, epilogue, false, stream);
+}
+
+extern "C" int zk_gemm_f16_ln_frag(const void *A, const void *W, void *C, int64_t M, int64_t N,
+                                   int64_t K, int64_t lda, int64_t ldw, const float *ln_part,
+                                   float ln_eps, const float *ln_s, const float *ln_c,
+                                   float *ln_out, void *stream) {
+  const char *who = "zk_gemm_f16_ln_frag";
+  if (N % 64) return fail(ZK_ERR_UNSUPPORTED, "%s: N must be a multiple of 64", who);
+  return gemm_f16_ln(who, A, W, C, M, N, K, lda, ldw, N, ln_part, ln_eps, ln_s, ln_c, ln_out,
+                     ZK_EPI_BIAS_GELU_ERF, true, stream);
 }
 
 // Shape / operand checks shared by the int8 entry points.
