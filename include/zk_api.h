@@ -359,6 +359,26 @@ int zk_gemm_i8_res_stats(const int8_t *A, const int8_t *W, void *C, int64_t M, i
                          const float *res_ln, const void *res_gamma, const void *res_beta,
                          float *part_out, void *stream);
 
+/* The INT8 FFN's intermediate in fragment order: the fp16 definition above
+ * with 32 int8 columns per k-step (lane l holds X[32 rb + l % 32][32 ks +
+ * 16 (l / 32) + e] at byte 16 l + e, e = 0 .. 15), the A operand of a
+ * 32x32x32 int8 MFMA. zk_gemm_i8_requant_frag writes zk_gemm_i8_requant's
+ * values (bit for bit) that way (ceil(M/32) * 32 x N bytes, rows past M not
+ * written; N a multiple of 128, Q 16-byte aligned); zk_gemm_i8_res_stats_frag
+ * is zk_gemm_i8_res_stats on such an A (K a multiple of 128; rows past M read
+ * and discarded; the 128x96 tile at every M, bit for bit with
+ * zk_gemm_i8_res_stats wherever that takes the same tile). No reference
+ * counterpart: the int8 intermediate between the reference's INT8 FFN
+ * linears (benchmarks/int8_bench.py:19-45) laid out for the second one. */
+int zk_gemm_i8_requant_frag(const int8_t *A, const int8_t *W, int8_t *Q, int64_t M, int64_t N,
+                            int64_t K, int64_t lda, int64_t ldw, float s_x, const float *s_w,
+                            const void *bias, int epilogue, float s_out, void *stream);
+int zk_gemm_i8_res_stats_frag(const int8_t *A, const int8_t *W, void *C, int64_t M, int64_t N,
+                              int64_t K, int64_t ldw, int64_t ldc, float s_x, const float *s_w,
+                              const void *bias, const void *res, int64_t ldr,
+                              const float *res_ln, const void *res_gamma, const void *res_beta,
+                              float *part_out, void *stream);
+
 /* c[r, :] = a[r, :] + b[b_rows == 1 ? 0 : r, :] for [rows, cols] contiguous
  * tensors in dtype ZK_F32 or ZK_F16 (fp16 summed in fp32, rounded once);
  * b_rows is 1 (row broadcast: bias) or rows.

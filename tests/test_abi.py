@@ -114,6 +114,16 @@ def test_library_exports_every_declared_symbol():
     (lambda lib: lib.zk_gemm_i8_res_stats(16, 16, 16, 8, 96, 64, 64, 64, 96, 1.0, 16, 16, None,
                                           96, None, None, None, 16, None),
      L.ZK_ERR_INVALID),  # no residual
+    (lambda lib: lib.zk_gemm_f16_res_stats_frag(16, 16, 16, 8, 96, 96, 96, 96, 16, 16, 96, None,
+                                                None, None, 16, None),
+     L.ZK_ERR_UNSUPPORTED),  # fragment-ordered A: K a multiple of 64
+    (lambda lib: lib.zk_gemm_f16_ln_frag(16, 16, 16, 8, 96, 96, 96, 96, 16, 1e-12, 16, 16, None,
+                                         None), L.ZK_ERR_UNSUPPORTED),  # N a multiple of 64
+    (lambda lib: lib.zk_gemm_i8_requant_frag(16, 16, 16, 8, 64, 64, 64, 64, 1.0, 16, 16, 2, 1.0,
+                                             None), L.ZK_ERR_UNSUPPORTED),  # N % 128
+    (lambda lib: lib.zk_gemm_i8_res_stats_frag(16, 16, 16, 8, 96, 64, 64, 96, 1.0, 16, 16, 16, 96,
+                                               None, None, None, 16, None),
+     L.ZK_ERR_UNSUPPORTED),  # fragment-ordered int8 A: K % 128
     (lambda lib: lib.zk_layernorm_q8_res_ln(16, 16, None, 16, 16, 16, 16, 16, 16, 4, 8, 1e-12,
                                             0.1, None), L.ZK_ERR_INVALID),  # no residual stats
     (lambda lib: lib.zk_layernorm_q8_res_ln(16, 16, 16, 16, 16, 16, 16, 16, 16, 4, 8, 1e-12,

@@ -13,8 +13,12 @@
   fragment order, on every tile configuration it runs (256x256, 256x192,
   128x128 and the 128x96 tile that replaces the 16x16-MFMA ones), and leaves
   the padding rows past M untouched.
+- The int8 pair: zk_gemm_i8_requant_frag writes zk_gemm_i8_requant's int8
+  values in fragment order (32 columns per k-step), bit for bit, rows past M
+  untouched; zk_gemm_i8_res_stats_frag gives zk_gemm_i8_res_stats's output
+  and statistics bit for bit on the same tile.
 - The folded encoder with and without the fragment-ordered FFN gives the same
-  output, bit for bit.
+  output, bit for bit, in fp16 and with the INT8 FFN.
 """
 
 import math
@@ -164,5 +168,85 @@ def test_encoder_frag_ffn_bit_identical(dev):
         torch.cuda.synchronize()
         if frag:
             assert enc._bufs["u_frag"] is not None
+        del enc
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
+def _i8(shape, tag):
+    return np.clip(np.rint(synthetic.normal(shape, tag=tag) * 40), -127, 127).astype(np.int8)
+
+
+@pytest.mark.parametrize("M,K,N", [(4096, 768, 3072), (1000, 768, 3072), (100, 256, 384),
+                                   (300, 128, 256)])
+def test_i8_requant_frag_matches_row_major(dev, M, K, N):
+    qa, qw = _t(_i8((M, K), 200), dev, torch.int8), _t(_i8((N, K), 201), dev, torch.int8)
+    sw = _t(np.abs(synthetic.normal((N,), tag=202, std=1e-3)) + 5e-4, dev, torch.float32)
+    b = _t(synthetic.round_f16(synthetic.normal((N,), tag=203, std=0.1)), dev)
+    s_x, s_out = 0.02, 6.0 / 127
+    q0 = torch.full((M, N), 99, dtype=torch.int8, device=dev)
+    Mp = -(-M // 32) * 32
+    q1 = torch.full((Mp * N,), 99, dtype=torch.int8, device=dev)
+    print(f"zk_gemm_i8_requant_frag M={M} K={K} N={N}", flush=True)
+    L.call("zk_gemm_i8_requant", qa.data_ptr(), qw.data_ptr(), q0.data_ptr(), M, N, K, K, K, N,
+           s_x, sw.data_ptr(), b.data_ptr(), L.ZK_EPI_BIAS_GELU_ERF, s_out, _stream())
+    L.call("zk_gemm_i8_requant_frag", qa.data_ptr(), qw.data_ptr(), q1.data_ptr(), M, N, K, K, K,
+           s_x, sw.data_ptr(), b.data_ptr(), L.ZK_EPI_BIAS_GELU_ERF, s_out, _stream())
+    torch.cuda.synchronize()
+    assert torch.equal(from_fragment_order(q1, M, N), q0)
+    if Mp > M:  # rows past M are not written
+        pad = q1.view(Mp // 32, N // 32, 2, 32, 16)[-1, :, :, M % 32:, :]
+        assert bool((pad == 99).all())
+
+
+@pytest.mark.parametrize("M,K,N", [(4096, 3072, 768), (1000, 3072, 768), (300, 256, 288)])
+@pytest.mark.parametrize("ln_res", [False, True])
+def test_i8_res_stats_frag_matches_row_major(dev, M, K, N, ln_res):
+    qa, qw = _t(_i8((M, K), 210), dev, torch.int8), _t(_i8((N, K), 211), dev, torch.int8)
+    sw = _t(np.abs(synthetic.normal((N,), tag=212, std=1e-4)) + 5e-5, dev, torch.float32)
+    b = _t(synthetic.round_f16(synthetic.normal((N,), tag=213, std=0.1)), dev)
+    res = _t(synthetic.round_f16(synthetic.normal((M, N), tag=214)), dev)
+    g = _t(synthetic.round_f16(1.0 + synthetic.normal((N,), tag=215, std=0.2)), dev)
+    be = _t(synthetic.round_f16(synthetic.normal((N,), tag=216, std=0.2)), dev)
+    r64 = res.double()
+    st = torch.stack([r64.mean(1), 1.0 / torch.sqrt(r64.var(1, unbiased=False) + EPS)], 1).float()
+    af = to_fragment_order(qa)
+    Mp = -(-M // 32) * 32
+    if Mp > M:  # padding rows: read, never stored
+        af.view(Mp // 32, K // 32, 2, 32, 16)[-1, :, :, M % 32:, :] = 127
+    outs = []
+    print(f"zk_gemm_i8_res_stats_frag M={M} K={K} N={N} ln_res={ln_res}", flush=True)
+    for frag in (False, True):
+        c = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+        part = torch.full((M, N // SEG, 2), float("nan"), dtype=torch.float32, device=dev)
+        ln = (st.data_ptr(), g.data_ptr(), be.data_ptr()) if ln_res else (None, None, None)
+        if frag:
+            L.call("zk_gemm_i8_res_stats_frag", af.data_ptr(), qw.data_ptr(), c.data_ptr(), M, N,
+                   K, K, N, 0.01, sw.data_ptr(), b.data_ptr(), res.data_ptr(), N, *ln,
+                   part.data_ptr(), _stream())
+        else:
+            L.call("zk_gemm_i8_res_stats", qa.data_ptr(), qw.data_ptr(), c.data_ptr(), M, N, K, K,
+                   K, N, 0.01, sw.data_ptr(), b.data_ptr(), res.data_ptr(), N, *ln,
+                   part.data_ptr(), _stream())
+        torch.cuda.synchronize()
+        outs.append((c, part))
+    (c0, p0), (c1, p1) = outs
+    assert not torch.isnan(c1).any()
+    assert torch.equal(c0.view(torch.int16), c1.view(torch.int16))
+    assert torch.equal(p0.view(torch.int32), p1.view(torch.int32))
+
+
+def test_encoder_int8_frag_ffn_bit_identical(dev):
+    layers = synthetic.bert_weights_wired(3, seed=9)
+    B, S = 32, 128
+    x = torch.from_numpy(synthetic.hidden_states(B, S, seed=9)).to(dev, torch.float16)
+    lens = torch.from_numpy(synthetic.padding_lengths(B, S)).to(dev)
+    outs = []
+    for frag in (True, False):
+        enc = BertEncoder(layers, device=dev)
+        enc.ffn_frag = frag
+        enc.enable_int8_ffn([0.05] * 3, [6.0 / 127] * 3, layers_fp32=layers)
+        outs.append(enc.forward(x, lens).clone())
+        torch.cuda.synchronize()
+        assert (enc._bufs["q_u_frag"] is not None) == frag
         del enc
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))

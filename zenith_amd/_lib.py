@@ -77,6 +77,10 @@ SIGNATURES: dict[str, list] = {
                            _vp, _i32, _f32, _vp],
     "zk_gemm_i8_res_stats": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _vp,
                              _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp],
+    "zk_gemm_i8_requant_frag": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp, _vp,
+                                _i32, _f32, _vp],
+    "zk_gemm_i8_res_stats_frag": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp, _vp,
+                                  _vp, _i64, _vp, _vp, _vp, _vp, _vp],
     "zk_gemm_workspace_size": [_i64, _i64, _i64, _i32],
     "zk_gemm_f16_ws": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
                        _vp, _vp, _i64, _i32, _vp, _i64, _vp],

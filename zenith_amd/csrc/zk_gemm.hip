@@ -460,9 +460,9 @@ void gemm_mfma_kernel(GemmParams p) {
   // APK: the tile's row blocks of the fragment-ordered A, (K / 16) KB each
   const int a_blocks = min(BM / 32, (p.M + 31) / 32 - m0 / 32);
   const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
-      APK ? (void *)((const char *)p.a_pk + (int64_t)(m0 / 32) * (p.K / 16) * 1024)
+      APK ? (void *)((const char *)p.a_pk + (int64_t)(m0 / 32) * (kbytes / 32) * 1024)
           : (void *)((const char *)p.A + (int64_t)m0 * lda_b),
-      (short)0, APK ? a_blocks * (p.K / 16) * 1024 : (int)((a_rows - 1) * lda_b + kbytes),
+      (short)0, APK ? a_blocks * (kbytes / 32) * 1024 : (int)((a_rows - 1) * lda_b + kbytes),
       0x00020000);
   const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
       (void *)((const char *)p.B + (int64_t)n0 * ldb_b), (short)0,
@@ -481,7 +481,7 @@ void gemm_mfma_kernel(GemmParams p) {
     if constexpr (APK) {
       const int f = wave * IA + g;
       chA[g] = 0;
-      offA[g] = ((f / KS) * (p.K / 16) + f % KS) * 1024 + lane * 16;
+      offA[g] = ((f / KS) * (kbytes / 32) + f % KS) * 1024 + lane * 16;
     } else {
       const int row = (wave * IA + g) * G::RPI + lane / CH;
       const int c = lds_slot<BKB>(row, lane % CH);  // the swizzle is an involution
@@ -511,7 +511,7 @@ void gemm_mfma_kernel(GemmParams p) {
   // buffer ks & 1 (KS is even), so the first k-step of the next slice can
   // be read while the last one of this slice is multiplied.
   Frag fa[2][TM], fb[2][TN];
-  static_assert(!APK || (MS == 32 && std::is_same<OP, F16Op>::value), "fragment-ordered A");
+  static_assert(!APK || (MS == 32 && !std::is_same<OP, F32Op>::value), "fragment-ordered A");
   constexpr int PER = IA + IB;  // DMA instructions per slice and wave
   auto rd = [&](int stage, int ks, int buf) {
     const char *As = smem + stage * G::STAGE;
@@ -802,9 +802,11 @@ void gemm_mfma_kernel(GemmParams p) {
     };
     constexpr int VPR = WTN / 8;  // 8-column vectors per stripe row
     // fragment-ordered output (p.c_pk): the folded-LayerNorm GELU epilogue of
-    // the fp16 32x32 tiles (FFN-up, whose output is FFN-down's A)
-    constexpr bool CPK = EPI == kEpiLnInGelu && MS == 32 && std::is_same<OutT, f16>::value &&
-                         WTN % 16 == 0;
+    // the fp16 32x32 tiles and the re-quantising int8 ones (FFN-up, whose
+    // output is FFN-down's A)
+    constexpr bool CPK = MS == 32 && ((EPI == kEpiLnInGelu && std::is_same<OutT, f16>::value &&
+                                       WTN % 16 == 0) ||
+                                      (Q8 && WTN % 32 == 0));
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       // LN_IN: (mean, rstd) of the rows this lane's registers hold
@@ -903,24 +905,43 @@ void gemm_mfma_kernel(GemmParams p) {
       };
       if constexpr (CPK) {
         if (p.c_pk) {
-          // C in fragment order: the stripe (32 rows, a whole row block) is
-          // WTN / 16 k-steps of the consumer's A, each 1 KB contiguous; lane l
-          // stores row l % 32, columns 8 (l / 32) .. +7 of the k-step
+          // C in fragment order: the stripe (32 rows, a whole row block) is a
+          // run of the consumer's 1 KB A fragments of KC columns (16 fp16 or
+          // 32 int8); lane l stores row l % 32, columns KE (l / 32) .. +KE-1
+          // of its fragment: 16 bytes
+          constexpr int KC = Q8 ? 32 : 16, KE = KC / 2;
           const int rl = lane & 31;
-          const int64_t blk = (int64_t)(row0 / 32) * (p.N / 16) + col0 / 16;
+          const int64_t blk = (int64_t)(row0 / 32) * (p.N / KC) + col0 / KC;
 #pragma unroll
-          for (int kc = 0; kc < WTN / 16; ++kc) {
-            const int cl = kc * 16 + (lane >> 5) * 8;
+          for (int kc = 0; kc < WTN / KC; ++kc) {
+            const int cl = kc * KC + (lane >> 5) * KE;
             if (row0 + rl < p.M && col0 + cl < p.N) {
               const float *src = ws + rl * G::EPITCH + cl;
-              const f32x4 lo = *(const f32x4 *)src, hi = *(const f32x4 *)(src + 4);
-              f16x8 h;
+              char *dst = (char *)p.C + ((blk + kc) * 64 + lane) * 16;
+              if constexpr (Q8) {
+                // rounded to fp16 first, as the row-major stores do
+                float of[2][8];
 #pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                h[e] = (f16)lo[e];
-                h[e + 4] = (f16)hi[e];
+                for (int h = 0; h < 2; ++h) {
+                  const f32x4 lo = *(const f32x4 *)(src + 8 * h), hi = *(const f32x4 *)(src + 8 * h + 4);
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) {
+                    of[h][e] = (float)(f16)lo[e];
+                    of[h][e + 4] = (float)(f16)hi[e];
+                  }
+                }
+                const u32x2 q0 = quant8(of[0], p.s_q, inv_q), q1 = quant8(of[1], p.s_q, inv_q);
+                store_nt((u32x4 *)dst, u32x4{q0[0], q0[1], q1[0], q1[1]});
+              } else {
+                const f32x4 lo = *(const f32x4 *)src, hi = *(const f32x4 *)(src + 4);
+                f16x8 h;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  h[e] = (f16)lo[e];
+                  h[e + 4] = (f16)hi[e];
+                }
+                store_nt((f16x8 *)dst, h);
               }
-              store_nt((f16x8 *)((f16 *)p.C + ((blk + kc) * 64 + lane) * 8), h);
             }
           }
           continue;
@@ -1044,9 +1065,10 @@ static bool launch_epi(GemmParams p, int epi, hipStream_t s) {
 // The residual + statistics epilogue on fragment-ordered A (p.a_pk): the
 // fp16 128x96 tile of 4 x 1 waves and 3-stage ring that FFN-down runs on
 // with row-major A.
+template <class OP, bool DEQ>
 static void launch_frag_res_stats(GemmParams p, hipStream_t s) {
   const int grid = tile_grid(p, 128, 96);
-  gemm_mfma_kernel<F16Op, 128, 96, 32, 128, 3, 4, 1, kEpiResStats, f16, false, true>
+  gemm_mfma_kernel<OP, 128, 96, 32, 128, 3, 4, 1, kEpiResStats, f16, DEQ, true>
       <<<grid, 256, 0, s>>>(p);
 }
 
@@ -1592,11 +1614,8 @@ static int res_stats_run(const char *who, GemmParams p, const float *res_ln, con
   p.res_beta = res_beta;
   p.part_out = part_out;
   if (p.a_pk) {
-    if constexpr (std::is_same<OP, F16Op>::value && !DEQ) {
-      launch_frag_res_stats(p, as_stream(stream));
-      return launched(true, who, kEpiResStats);
-    }
-    return fail(ZK_ERR_UNSUPPORTED, "%s: fragment-ordered A is fp16 only", who);
+    launch_frag_res_stats<OP, DEQ>(p, as_stream(stream));
+    return launched(true, who, kEpiResStats);
   }
   const int64_t t192 = (M + 255) / 256 * (N / 192);
   const bool ok = launch_mfma<OP, f16, DEQ>(p, kEpiResStats, as_stream(stream),
@@ -1768,6 +1787,50 @@ extern "C" int zk_gemm_i8_requant(const int8_t *A, const int8_t *W, int8_t *Q, i
   p.s_q = s_out;
   return launched(launch_mfma<I8Op, int8_t, true>(p, epilogue, as_stream(stream)),
                   "zk_gemm_i8_requant", epilogue);
+}
+
+extern "C" int zk_gemm_i8_requant_frag(const int8_t *A, const int8_t *W, int8_t *Q, int64_t M,
+                                       int64_t N, int64_t K, int64_t lda, int64_t ldw,
+                                       float s_x, const float *s_w, const void *bias,
+                                       int epilogue, float s_out, void *stream) {
+  const char *who = "zk_gemm_i8_requant_frag";
+  int st = check_i8(who, A, W, Q, M, N, K, lda, ldw, N, epilogue);
+  if (st || M == 0 || N == 0) return st;
+  if (N % 128) return fail(ZK_ERR_UNSUPPORTED, "%s: N must be a multiple of 128", who);
+  if (epilogue == ZK_EPI_BIAS_RESIDUAL)
+    return fail(ZK_ERR_INVALID, "%s: no residual epilogue for int8 output", who);
+  if (!s_w) return fail(ZK_ERR_INVALID, "%s: s_w is required", who);
+  if (!(s_x > 0.f) || !(s_out > 0.f)) return fail(ZK_ERR_INVALID, "%s: s_x and s_out must be > 0", who);
+  if (epilogue != ZK_EPI_NONE && !bias) return fail(ZK_ERR_INVALID, "%s: epilogue needs a bias", who);
+  if (!aligned16(Q)) return fail(ZK_ERR_UNSUPPORTED, "%s: Q must be 16-byte aligned", who);
+  GemmParams p{A, W, Q, (int)M, (int)N, (int)K, lda, ldw, N, bias, nullptr, 0, s_x, s_w, 0};
+  p.s_q = s_out;
+  p.c_pk = 1;
+  // every 32x32-MFMA tile (0, 1, 4, 5) has the fragment-ordered store; the
+  // 16x16 ones (2, 3) give way to the 128x96 tile
+  int cfg = pick_cfg(p.M, p.N, p.K);
+  if (cfg == 2 || cfg == 3) cfg = 4;
+  return launched(launch_mfma<I8Op, int8_t, true>(p, epilogue, as_stream(stream), cfg), who,
+                  epilogue);
+}
+
+extern "C" int zk_gemm_i8_res_stats_frag(const int8_t *A, const int8_t *W, void *C, int64_t M,
+                                         int64_t N, int64_t K, int64_t ldw, int64_t ldc,
+                                         float s_x, const float *s_w, const void *bias,
+                                         const void *res, int64_t ldr, const float *res_ln,
+                                         const void *res_gamma, const void *res_beta,
+                                         float *part_out, void *stream) {
+  const char *who = "zk_gemm_i8_res_stats_frag";
+  int st = check_i8(who, A, W, C, M, N, K, K, ldw, ldc, ZK_EPI_BIAS);
+  if (st || M == 0 || N == 0) return st;
+  if (K % 128) return fail(ZK_ERR_UNSUPPORTED, "%s: K must be a multiple of 128", who);
+  if (!aligned16(A)) return fail(ZK_ERR_UNSUPPORTED, "%s: A must be 16-byte aligned", who);
+  if (!s_w || !(s_x > 0.f)) return fail(ZK_ERR_INVALID, "%s: s_w and s_x > 0 are required", who);
+  if (ldc % 8 || !aligned16(C))
+    return fail(ZK_ERR_UNSUPPORTED, "%s: ldc must be a multiple of 8 and C 16-byte aligned", who);
+  GemmParams p{A, W, C, (int)M, (int)N, (int)K, K, ldw, ldc, bias, res, ldr, s_x, s_w, 0};
+  p.a_pk = A;
+  return res_stats_run<I8Op, true>(who, p, res_ln, res_gamma, res_beta, part_out, stream);
 }
 
 // Epilogue of the SIMT fp32 path, in place on C: the same operations, in the

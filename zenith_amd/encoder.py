@@ -57,23 +57,25 @@ FFN_PAD = 192
 
 
 def to_fragment_order(x: torch.Tensor) -> torch.Tensor:
-    """x [R, K] (fp16, K a multiple of 16) in fragment order, the layout of
-    zk_gemm_f16_ln_frag's output and zk_gemm_f16_res_stats_frag's A: for row
-    block rb and k-step ks, 64 lanes x 8 halves, lane l holding
-    x[32 rb + l % 32, 16 ks + 8 (l // 32) .. +7]. Rows are zero-padded to a
-    multiple of 32; returned flat."""
+    """x [R, K] in fragment order, the layout of the *_frag entry points'
+    FFN intermediate: for row block rb and k-step ks (E = 8 fp16 or 16 int8
+    values per lane, 2 E per k-step; K a multiple of 2 E), 64 lanes x 16
+    bytes, lane l holding x[32 rb + l % 32, 2 E ks + E (l // 32) .. +E-1].
+    Rows are zero-padded to a multiple of 32; returned flat."""
     R, K = x.shape
+    E = 16 // x.element_size()
     Rp = -(-R // 32) * 32
     xp = torch.zeros((Rp, K), dtype=x.dtype, device=x.device)
     xp[:R] = x
-    return xp.reshape(Rp // 32, 32, K // 16, 2, 8).permute(0, 2, 3, 1, 4).reshape(-1).contiguous()
+    return xp.reshape(Rp // 32, 32, K // (2 * E), 2, E).permute(0, 2, 3, 1, 4).reshape(-1).contiguous()
 
 
 def from_fragment_order(p: torch.Tensor, R: int, K: int) -> torch.Tensor:
     """The [R, K] matrix held in fragment order by p (inverse of
     to_fragment_order)."""
+    E = 16 // p.element_size()
     Rp = -(-R // 32) * 32
-    x = p[:Rp * K].reshape(Rp // 32, K // 16, 2, 32, 8).permute(0, 3, 1, 2, 4).reshape(Rp, K)
+    x = p[:Rp * K].reshape(Rp // 32, K // (2 * E), 2, 32, E).permute(0, 3, 1, 2, 4).reshape(Rp, K)
     return x[:R]
 
 
@@ -216,7 +218,9 @@ class BertEncoder:
         would run the 128x96 tile, i.e. unless M >= 1024 and its 256x192
         tiles number at least 160 (s512 at b32). FFN-up then stores whole
         1 KB blocks instead of 192-byte row pieces (27.4 against 28.4 us at
-        b32 s128), and the encoder step is 1.3% faster."""
+        b32 s128), and the encoder step is 1.3% faster. The INT8 FFN does the
+        same with its int8 intermediate (zk_gemm_i8_requant_frag,
+        zk_gemm_i8_res_stats_frag; FFN a multiple of 128)."""
         H = self.hidden
         t192 = -(-M // 256) * (H // 192) if H % 192 == 0 else 0
         return (self.ffn_frag and self.fold_ln and self.ffn % 64 == 0
@@ -297,6 +301,8 @@ class BertEncoder:
                 # blocks; the rows past M stay zero)
                 "u_frag": (torch.zeros(-(-M // 32) * 32 * I, dtype=F16, device=d)
                            if self.frag_ffn(M) else None),
+                "q_u_frag": (torch.zeros(-(-M // 32) * 32 * I, dtype=torch.int8, device=d)
+                             if self.frag_ffn(M) and I % 128 == 0 else None),
             })
         self._graph = None
         return self._bufs
@@ -469,15 +475,27 @@ class BertEncoder:
                            prev["ln2_g"].data_ptr(), prev["ln2_b"].data_ptr(),
                            w["ln1_g"].data_ptr(), w["ln1_b"].data_ptr(), h.data_ptr(),
                            qh.data_ptr(), M, H, self.eps, q["s_x"], stream)
-                # 5. FFN-up int8 + bias + GELU, re-quantised
-                L.call("zk_gemm_i8_requant", qh.data_ptr(), q["Wi_q"].data_ptr(), qu.data_ptr(), M,
-                       I, H, H, H, qu.stride(0), q["s_x"], q["s_wi"].data_ptr(),
-                       w["bi"].data_ptr(), self.gelu_epi, q["s_h"], stream)
-                # 6. FFN-down int8 + bias + h -> h2, stats
-                L.call("zk_gemm_i8_res_stats", qu.data_ptr(), q["Wo2_q"].data_ptr(), h2.data_ptr(),
-                       M, H, I, qu.stride(0), q["Wo2_q"].stride(0), H, q["s_h"],
-                       q["s_wo2"].data_ptr(), w["bo2"].data_ptr(), h.data_ptr(), H, None, None,
-                       None, p2.data_ptr(), stream)
+                qf = bf.get("q_u_frag")
+                if qf is not None:
+                    # 5-6. the same, the int8 intermediate in fragment order
+                    L.call("zk_gemm_i8_requant_frag", qh.data_ptr(), q["Wi_q"].data_ptr(),
+                           qf.data_ptr(), M, I, H, H, H, q["s_x"], q["s_wi"].data_ptr(),
+                           w["bi"].data_ptr(), self.gelu_epi, q["s_h"], stream)
+                    L.call("zk_gemm_i8_res_stats_frag", qf.data_ptr(), q["Wo2_q"].data_ptr(),
+                           h2.data_ptr(), M, H, I, q["Wo2_q"].stride(0), H, q["s_h"],
+                           q["s_wo2"].data_ptr(), w["bo2"].data_ptr(), h.data_ptr(), H, None,
+                           None, None, p2.data_ptr(), stream)
+                else:
+                    # 5. FFN-up int8 + bias + GELU, re-quantised
+                    L.call("zk_gemm_i8_requant", qh.data_ptr(), q["Wi_q"].data_ptr(),
+                           qu.data_ptr(), M, I, H, H, H, qu.stride(0), q["s_x"],
+                           q["s_wi"].data_ptr(), w["bi"].data_ptr(), self.gelu_epi, q["s_h"],
+                           stream)
+                    # 6. FFN-down int8 + bias + h -> h2, stats
+                    L.call("zk_gemm_i8_res_stats", qu.data_ptr(), q["Wo2_q"].data_ptr(),
+                           h2.data_ptr(), M, H, I, qu.stride(0), q["Wo2_q"].stride(0), H,
+                           q["s_h"], q["s_wo2"].data_ptr(), w["bo2"].data_ptr(), h.data_ptr(), H,
+                           None, None, None, p2.data_ptr(), stream)
             cur, cur_parts = h2, p2
         w = self.layers[stop - 1]
         L.call("zk_layernorm", cur.data_ptr(), None, w["ln2_g"].data_ptr(), w["ln2_b"].data_ptr(),
