@@ -186,6 +186,43 @@ def kernel_cases(torch, dev):
                 "TOP/s", "int8", "mfma", f"M={M} K={K} N={N}"
         return setup
 
+    def ffn_i8_frag(M=4096, H=768, I=3072):
+        """The INT8-FFN encoder's FFN at b32 s128 with the int8 intermediate
+        in fragment order: the re-quantising FFN-up writing it
+        (zk_gemm_i8_requant_frag), or FFN-down + residual + statistics reading
+        it (zk_gemm_i8_res_stats_frag), with the scales of gemm_i8 and
+        res_stats_i8."""
+        def up():
+            a = torch.randint(-127, 128, (M, H), dtype=torch.int8, device=dev)
+            w = torch.randint(-127, 128, (I, H), dtype=torch.int8, device=dev)
+            sw = torch.full((I,), 1e-3, dtype=torch.float32, device=dev)
+            b = torch.zeros(I, dtype=f16, device=dev)
+            c = torch.empty(-(-M // 32) * 32 * I, dtype=torch.int8, device=dev)
+            keep = (a, w, sw, b, c)
+            args = (a.data_ptr(), w.data_ptr(), c.data_ptr(), M, I, H, H, H, 0.01, sw.data_ptr(),
+                    b.data_ptr(), L.ZK_EPI_BIAS_GELU_ERF, 6.0 / 127)
+            return (lambda i: _rc(L, lib.zk_gemm_i8_requant_frag(*args, s())) and keep), \
+                2.0 * M * I * H, "TOP/s", "int8", "mfma", \
+                f"M={M} K={H} N={I} int8 out in fragment order"
+
+        def down():
+            from zenith_amd.encoder import to_fragment_order
+            a = torch.randint(-127, 128, (M, I), dtype=torch.int8, device=dev)
+            af = to_fragment_order(a)
+            w = torch.randint(-127, 128, (H, I), dtype=torch.int8, device=dev)
+            sw = torch.full((H,), 1e-3, dtype=torch.float32, device=dev)
+            b = torch.zeros(H, dtype=f16, device=dev)
+            r = torch.from_numpy(synthetic.normal((M, H), tag=3)).to(dev, f16)
+            c = torch.empty((M, H), dtype=f16, device=dev)
+            part = torch.empty((M, H // 96, 2), dtype=torch.float32, device=dev)
+            keep = (a, af, w, sw, b, r, c, part)
+            args = (af.data_ptr(), w.data_ptr(), c.data_ptr(), M, H, I, I, H, 0.01, sw.data_ptr(),
+                    b.data_ptr(), r.data_ptr(), H, None, None, None, part.data_ptr())
+            return (lambda i: _rc(L, lib.zk_gemm_i8_res_stats_frag(*args, s())) and keep), \
+                2.0 * M * H * I, "TOP/s", "int8", "mfma", \
+                f"M={M} K={I} N={H} + residual + row statistics, A in fragment order"
+        return up, down
+
     def res_stats_i8(M, K, N):
         """The INT8-FFN encoder's FFN-down with LayerNorm 2 folded: int8
         product, dequantisation, bias, the residual LayerNorm-ed on the fly,
@@ -491,6 +528,10 @@ def kernel_cases(torch, dev):
         "int8_ffn_down": gemm_i8(4096, 3072, 768, E),
         # the INT8-FFN layer's own launches at b32 s128 (LayerNorm 2 folded)
         "int8_ffn_down_res_stats": res_stats_i8(4096, 3072, 768),
+        # the same FFN with the int8 intermediate in fragment order, as the
+        # INT8-FFN encoder runs it at b32 s128
+        "int8_ffn_up_frag": ffn_i8_frag()[0],
+        "int8_ffn_down_res_stats_frag": ffn_i8_frag()[1],
         "add_layernorm_q8_res_ln": add_ln_q8_res_ln(),
         "add_layernorm": add_ln(),
         "bias_gelu": bias_gelu(),

@@ -205,6 +205,18 @@ int zk_qkv_attn_f16_ln(const void *X, const void *Wqkv, const float *ln_part, fl
                        int64_t batch, int64_t seq, int64_t hidden, int64_t heads,
                        const int32_t *valid_lens, float scale, void *stream);
 
+/* zk_qkv_attn_f16 (ln_part NULL, bqkv used) or zk_qkv_attn_f16_ln (ln_part
+ * set, bqkv ignored) with ctx written in fragment order (defined below, at
+ * zk_gemm_f16_ln_frag: ceil(B*S/32) * 32 x hidden halves, rows past B*S not
+ * written, 16-byte aligned), the A operand of zk_gemm_f16_res_stats_frag for
+ * the out-projection. The values are those entry points', bit for bit. No
+ * reference counterpart (the layout of the attention output the reference
+ * hands to its out-projection, benchmarks/bert_fp16_full.py:118-126). */
+int zk_qkv_attn_f16_frag(const void *X, const void *Wqkv, const void *bqkv, const float *ln_part,
+                         float ln_eps, const float *ln_s, const float *ln_c, float *ln_out,
+                         void *ctx, int64_t batch, int64_t seq, int64_t hidden, int64_t heads,
+                         const int32_t *valid_lens, float scale, void *stream);
+
 /* fp16 GEMM with a residual and the row statistics of its output:
  *   C = A[M,K] . W[N,K]^T + bias + R,  R = res, or with res_ln [M][2]
  *       (mean, rstd per row): R = (res - mean) rstd gamma + beta

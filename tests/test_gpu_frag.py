@@ -17,8 +17,10 @@
   values in fragment order (32 columns per k-step), bit for bit, rows past M
   untouched; zk_gemm_i8_res_stats_frag gives zk_gemm_i8_res_stats's output
   and statistics bit for bit on the same tile.
-- The folded encoder with and without the fragment-ordered FFN gives the same
-  output, bit for bit, in fp16 and with the INT8 FFN.
+- zk_qkv_attn_f16_frag writes zk_qkv_attn_f16's / zk_qkv_attn_f16_ln's
+  attention output, bit for bit, in fragment order (padding rows untouched).
+- The folded encoder with and without the fragment-ordered FFN and attention
+  output gives the same output, bit for bit, in fp16 and with the INT8 FFN.
 """
 
 import math
@@ -250,3 +252,40 @@ def test_encoder_int8_frag_ffn_bit_identical(dev):
         assert (enc._bufs["q_u_frag"] is not None) == frag
         del enc
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
+@pytest.mark.parametrize("B,S", [(32, 128), (5, 128), (3, 64)])
+@pytest.mark.parametrize("ln", [False, True])
+def test_qkv_attn_frag_matches_row_major(dev, B, S, ln):
+    heads, H = 12, 768
+    M = B * S
+    x = _t(synthetic.round_f16(synthetic.normal((M, H), tag=220)), dev)
+    w = _t(synthetic.round_f16(synthetic.normal((3 * H, H), tag=221, std=0.05)), dev)
+    b = _t(synthetic.round_f16(synthetic.normal((3 * H,), tag=222, std=0.1)), dev)
+    lens = torch.from_numpy(synthetic.padding_lengths(B, S)).to(dev)
+    xn = x.double().cpu().numpy().reshape(M, H // SEG, SEG)
+    mean = xn.mean(-1)
+    part = _t(np.stack([mean, ((xn - mean[..., None]) ** 2).sum(-1)], -1), dev, torch.float32)
+    sc = _t(synthetic.normal((3 * H,), tag=223, std=0.1), dev, torch.float32)
+    cc = _t(synthetic.normal((3 * H,), tag=224, std=0.1), dev, torch.float32)
+    Mp = -(-M // 32) * 32
+    c0 = torch.full((M, H), float("nan"), dtype=torch.float16, device=dev)
+    c1 = torch.full((Mp * H,), 7.0, dtype=torch.float16, device=dev)
+    scale = 1.0 / math.sqrt(64)
+    print(f"zk_qkv_attn_f16_frag B={B} S={S} ln={ln}", flush=True)
+    if ln:
+        L.call("zk_qkv_attn_f16_ln", x.data_ptr(), w.data_ptr(), part.data_ptr(), EPS,
+               sc.data_ptr(), cc.data_ptr(), None, c0.data_ptr(), B, S, H, heads, lens.data_ptr(),
+               scale, _stream())
+    else:
+        L.call("zk_qkv_attn_f16", x.data_ptr(), w.data_ptr(), b.data_ptr(), c0.data_ptr(), B, S,
+               H, heads, lens.data_ptr(), scale, _stream())
+    L.call("zk_qkv_attn_f16_frag", x.data_ptr(), w.data_ptr(), b.data_ptr(),
+           part.data_ptr() if ln else None, EPS, sc.data_ptr() if ln else None,
+           cc.data_ptr() if ln else None, None, c1.data_ptr(), B, S, H, heads, lens.data_ptr(),
+           scale, _stream())
+    torch.cuda.synchronize()
+    assert torch.equal(from_fragment_order(c1, M, H).view(torch.int16), c0.view(torch.int16))
+    if Mp > M:
+        pad = c1.view(Mp // 32, H // 16, 2, 32, 8)[-1, :, :, M % 32:, :]
+        assert bool((pad == 7.0).all())

@@ -57,6 +57,8 @@ SIGNATURES: dict[str, list] = {
     "zk_qkv_attn_f16": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _f32, _vp],
     "zk_qkv_attn_f16_ln": [_vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp,
                            _f32, _vp],
+    "zk_qkv_attn_f16_frag": [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
+                             _i64, _vp, _f32, _vp],
     "zk_gemm_f16_res_stats": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64,
                               _vp, _vp, _vp, _vp, _vp],
     "zk_gemm_f16_ln": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _f32, _vp, _vp,

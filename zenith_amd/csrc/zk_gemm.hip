@@ -746,8 +746,46 @@ void gemm_mfma_kernel(GemmParams p) {
         attn32_pv<HD, true, HD>(Vt + off1, pf1, lane, o);
       }
       const int grow = m0 + qr;
-      if (grow < p.M) {
-        const float inv = l > 0.f ? 1.0f / l : 0.f;
+      const float inv = l > 0.f ? 1.0f / l : 0.f;
+      // (f16)as_f32(o inv) in both layouts: the product rounded to fp32, then
+      // to fp16, so that no build fuses it into one rounding in one of them
+      if (p.c_pk) {
+        // ctx in fragment order (the out-projection's A): the wave's 32 rows
+        // are one row block, head tn's 64 columns four 1 KB k-steps. Lane l
+        // holds columns 8 g + 4 (l / 32) .. +3 of each 32-column group; one
+        // v_permlane32_swap per register pair hands each half of the wave
+        // the other half's 4 columns, so that lane l holds columns
+        // 8 (l / 32) .. +7 of a k-step (16 bytes, one store per k-step).
+        char *F = (char *)p.C + ((int64_t)((m0 + wave * 32) / 32) * (p.ldc / 16) + tn * (HD / 16)) * 1024 +
+                  lane * 16;
+#pragma unroll
+        for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+          for (int kh = 0; kh < 2; ++kh) {
+            u32x2 a, b;  // columns 16 kh + 4 (l / 32) and 16 kh + 8 + 4 (l / 32), 4 each
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const f16 a0 = (f16)as_f32(o[dt][8 * kh + 2 * e] * inv);
+              const f16 a1 = (f16)as_f32(o[dt][8 * kh + 2 * e + 1] * inv);
+              const f16 b0 = (f16)as_f32(o[dt][8 * kh + 4 + 2 * e] * inv);
+              const f16 b1 = (f16)as_f32(o[dt][8 * kh + 4 + 2 * e + 1] * inv);
+              a[e] = (unsigned)__builtin_bit_cast(unsigned short, a0) |
+                     ((unsigned)__builtin_bit_cast(unsigned short, a1) << 16);
+              b[e] = (unsigned)__builtin_bit_cast(unsigned short, b0) |
+                     ((unsigned)__builtin_bit_cast(unsigned short, b1) << 16);
+            }
+            // upper lanes' a <-> lower lanes' b: the lower half then holds
+            // columns 0-7 of the k-step in (a, b), the upper half 8-15
+            u32x4 v;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const auto sw = __builtin_amdgcn_permlane32_swap(a[e], b[e], false, false);
+              v[e] = sw[0];
+              v[e + 2] = sw[1];
+            }
+            if (grow < p.M) store_nt((u32x4 *)(F + (dt * 2 + kh) * 1024), v);
+          }
+      } else if (grow < p.M) {
         f16 *O = (f16 *)p.C + (int64_t)grow * p.ldc + tn * HD;
 #pragma unroll
         for (int dt = 0; dt < HD / 32; ++dt)
@@ -755,7 +793,7 @@ void gemm_mfma_kernel(GemmParams p) {
           for (int g = 0; g < 4; ++g) {
             f16x4 out;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) out[e] = (f16)(o[dt][4 * g + e] * inv);
+            for (int e = 0; e < 4; ++e) out[e] = (f16)as_f32(o[dt][4 * g + e] * inv);
             *(f16x4 *)(O + dt * 32 + 8 * g + 4 * h32) = out;
           }
       }
@@ -1512,7 +1550,7 @@ static int qkv_attn_impl(const char *who, const void *X, const void *Wqkv, const
                          const float *ln_part, float ln_eps, const float *ln_s,
                          const float *ln_c, float *ln_out, void *ctx, int64_t batch,
                          int64_t seq, int64_t hidden, int64_t heads, const int32_t *valid_lens,
-                         float scale, void *stream) {
+                         float scale, void *stream, bool frag = false) {
   if (batch < 0 || seq <= 0 || hidden <= 0 || heads <= 0)
     return fail(ZK_ERR_INVALID, "%s: bad size", who);
   if (batch == 0) return ZK_OK;
@@ -1538,6 +1576,8 @@ static int qkv_attn_impl(const char *who, const void *X, const void *Wqkv, const
   if (st) return st;
   if (!aligned16(X) || !aligned16(Wqkv) || !aligned8(ctx))
     return fail(ZK_ERR_UNSUPPORTED, "%s: X and Wqkv must be 16-byte, ctx 8-byte aligned", who);
+  if (frag && !aligned16(ctx))
+    return fail(ZK_ERR_UNSUPPORTED, "%s: ctx in fragment order must be 16-byte aligned", who);
   if ((st = check_span(who, K, K, K, 2))) return st;
   GemmParams p{X, Wqkv, ctx, (int)M, (int)N, (int)K, K, K, hidden, bqkv, nullptr, 0, 1.f, nullptr, 0};
   p.seq = (int)seq;
@@ -1550,6 +1590,7 @@ static int qkv_attn_impl(const char *who, const void *X, const void *Wqkv, const
   p.ln_s = ln_s;
   p.ln_c = ln_c;
   p.ln_out = ln_out;
+  p.c_pk = frag;
   launch_qkv_attn(p, as_stream(stream));
   return check_launch(who);
 }
@@ -1569,6 +1610,16 @@ extern "C" int zk_qkv_attn_f16_ln(const void *X, const void *Wqkv, const float *
   if (!ln_part) return fail(ZK_ERR_INVALID, "zk_qkv_attn_f16_ln: null statistics");
   return qkv_attn_impl("zk_qkv_attn_f16_ln", X, Wqkv, nullptr, ln_part, ln_eps, ln_s, ln_c,
                        ln_out, ctx, batch, seq, hidden, heads, valid_lens, scale, stream);
+}
+
+extern "C" int zk_qkv_attn_f16_frag(const void *X, const void *Wqkv, const void *bqkv,
+                                    const float *ln_part, float ln_eps, const float *ln_s,
+                                    const float *ln_c, float *ln_out, void *ctx, int64_t batch,
+                                    int64_t seq, int64_t hidden, int64_t heads,
+                                    const int32_t *valid_lens, float scale, void *stream) {
+  return qkv_attn_impl("zk_qkv_attn_f16_frag", X, Wqkv, ln_part ? nullptr : bqkv, ln_part,
+                       ln_eps, ln_s, ln_c, ln_out, ctx, batch, seq, hidden, heads, valid_lens,
+                       scale, stream, true);
 }
 
 // Operand checks of the folded-LayerNorm GEMMs: fp16, W[N,K], dense-enough

@@ -142,8 +142,10 @@ class BertEncoder:
         self.fold_ln = (bool(fold_layernorm) and gelu == "erf" and self.hidden % 96 == 0
                         and self.hidden <= 1536)
         # the folded fp16 FFN passes its intermediate in fragment order where
-        # it can (see frag_ffn); read when the buffers are made
+        # it can (see frag_ffn), and so does the fused attention its output;
+        # read when the buffers are made
         self.ffn_frag = True
+        self.attn_frag = True
         d = self.device
         self.layers = []
         for i, w in enumerate(layers):
@@ -303,6 +305,11 @@ class BertEncoder:
                            if self.frag_ffn(M) else None),
                 "q_u_frag": (torch.zeros(-(-M // 32) * 32 * I, dtype=torch.int8, device=d)
                              if self.frag_ffn(M) and I % 128 == 0 else None),
+                # the attention output in fragment order (fp16 layers with
+                # the fused QKV + attention launch)
+                "ctx_frag": (torch.zeros(-(-M // 32) * 32 * H, dtype=F16, device=d)
+                             if self.attn_frag and self.frag_ffn(M) and self.fused_attention(S, B)
+                             else None),
             })
         self._graph = None
         return self._bufs
@@ -413,7 +420,17 @@ class BertEncoder:
             prev = None if first else self.layers[i - 1]
             h2, p2 = (bf["ping"], bf["p2a"]) if i % 2 == 0 else (bf["pong"], bf["p2b"])
             # 1-2. QKV projection (+ LN2 of the previous layer) and attention
-            if self.fused_attention(S, B):
+            cf = bf.get("ctx_frag") if self.int8 is None else None
+            if cf is not None:
+                # ctx in fragment order for the out-projection below
+                L.call("zk_qkv_attn_f16_frag", cur.data_ptr(),
+                       w["Wqkv" if first else "Wqkv_f"].data_ptr(), w["bqkv"].data_ptr(),
+                       None if first else cur_parts.data_ptr(), self.eps,
+                       None if first else w["s_qkv"].data_ptr(),
+                       None if first else w["c_qkv"].data_ptr(),
+                       None if first else mr2.data_ptr(), cf.data_ptr(), B, S, H, nh, lp, scale,
+                       stream)
+            elif self.fused_attention(S, B):
                 if first:
                     L.call("zk_qkv_attn_f16", cur.data_ptr(), w["Wqkv"].data_ptr(),
                            w["bqkv"].data_ptr(), ctx.data_ptr(), B, S, H, nh, lp, scale, stream)
@@ -433,11 +450,18 @@ class BertEncoder:
                 self._attention(qkv, ctx, lens, B, S, stream)
             if self.int8 is None:
                 # 3. out-projection + residual (the input, or LN2(input)) -> h, stats
-                L.call("zk_gemm_f16_res_stats", ctx.data_ptr(), w["Wo"].data_ptr(), h.data_ptr(),
-                       M, H, H, H, H, H, w["bo"].data_ptr(), cur.data_ptr(), H,
-                       None if first else mr2.data_ptr(),
-                       None if first else prev["ln2_g"].data_ptr(),
-                       None if first else prev["ln2_b"].data_ptr(), p1.data_ptr(), stream)
+                if cf is not None:
+                    L.call("zk_gemm_f16_res_stats_frag", cf.data_ptr(), w["Wo"].data_ptr(),
+                           h.data_ptr(), M, H, H, H, H, w["bo"].data_ptr(), cur.data_ptr(), H,
+                           None if first else mr2.data_ptr(),
+                           None if first else prev["ln2_g"].data_ptr(),
+                           None if first else prev["ln2_b"].data_ptr(), p1.data_ptr(), stream)
+                else:
+                    L.call("zk_gemm_f16_res_stats", ctx.data_ptr(), w["Wo"].data_ptr(),
+                           h.data_ptr(), M, H, H, H, H, H, w["bo"].data_ptr(), cur.data_ptr(), H,
+                           None if first else mr2.data_ptr(),
+                           None if first else prev["ln2_g"].data_ptr(),
+                           None if first else prev["ln2_b"].data_ptr(), p1.data_ptr(), stream)
                 uf = bf.get("u_frag")
                 if uf is not None:
                     # 4-5. the same, the intermediate in fragment order
