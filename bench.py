@@ -363,6 +363,31 @@ def kernel_cases(torch, dev):
                 (f", output rows of {2 * (N + pad)} bytes as in the encoder" if pad else "")
         return setup
 
+    def out_proj_frag(M=4096, H=768):
+        """The fp16 encoder's out-projection: A (the attention output) in
+        fragment order, bias + residual LayerNorm + statistics
+        (zk_gemm_f16_res_stats_frag)."""
+        def setup():
+            from zenith_amd.encoder import to_fragment_order
+            a = torch.from_numpy(synthetic.uniform((M, H), tag=1)).to(dev, f16)
+            af = to_fragment_order(a)
+            w = torch.from_numpy(synthetic.uniform((H, H), tag=2)).to(dev, f16) * 0.05
+            b = torch.zeros(H, dtype=f16, device=dev)
+            r = torch.from_numpy(synthetic.normal((M, H), tag=3)).to(dev, f16)
+            c = torch.empty((M, H), dtype=f16, device=dev)
+            ms = torch.zeros((M, 2), dtype=torch.float32, device=dev)
+            ms[:, 1] = 1.0
+            g = torch.ones(H, dtype=f16, device=dev)
+            be = torch.zeros(H, dtype=f16, device=dev)
+            part = torch.empty((M, H // 96, 2), dtype=torch.float32, device=dev)
+            keep = (a, af, w, b, r, c, ms, g, be, part)
+            args = (af.data_ptr(), w.data_ptr(), c.data_ptr(), M, H, H, H, H, b.data_ptr(),
+                    r.data_ptr(), H, ms.data_ptr(), g.data_ptr(), be.data_ptr(), part.data_ptr())
+            return (lambda i: _rc(L, lib.zk_gemm_f16_res_stats_frag(*args, s())) and keep), \
+                2.0 * M * H * H, "TFLOP/s", "fp16", "mfma", \
+                f"M={M} K={H} N={H} + residual LayerNorm + row statistics, A in fragment order"
+        return setup
+
     def ffn_frag(M=4096, H=768, I=3072, pad=FFN_PAD):
         """The encoder's FFN at b32 s128 with its intermediate in fragment
         order: FFN-up on the folded LayerNorm + GELU writing it
@@ -407,9 +432,10 @@ def kernel_cases(torch, dev):
                 f"M={M} K={I} N={H} + residual LayerNorm + row statistics, A in fragment order"
         return up, down
 
-    def qkv_attn_ln(B=32, S=128, heads=12):
+    def qkv_attn_ln(B=32, S=128, heads=12, frag=False):
         """The encoder's fused QKV projection + attention with the previous
-        layer's LayerNorm folded in (layers 2-12 at s128)."""
+        layer's LayerNorm folded in (layers 2-12 at s128); frag: the output in
+        fragment order, as the fp16 encoder writes it (zk_qkv_attn_f16_frag)."""
         def setup():
             H = heads * 64
             x = torch.from_numpy(synthetic.normal((B * S, H), tag=70)).to(dev, f16)
@@ -419,15 +445,21 @@ def kernel_cases(torch, dev):
             sc = torch.zeros(3 * H, dtype=torch.float32, device=dev)
             cc = torch.zeros(3 * H, dtype=torch.float32, device=dev)
             mr = torch.empty((B * S, 2), dtype=torch.float32, device=dev)
-            ctx = torch.empty((B * S, H), dtype=f16, device=dev)
+            ctx = torch.empty((-(-B * S // 32) * 32, H), dtype=f16, device=dev)
             lens = torch.from_numpy(synthetic.padding_lengths(B, S)).to(dev)
             keep = (x, w, part, sc, cc, mr, ctx, lens)
-            args = (x.data_ptr(), w.data_ptr(), part.data_ptr(), 1e-12, sc.data_ptr(),
-                    cc.data_ptr(), mr.data_ptr(), ctx.data_ptr(), B, S, H, heads,
-                    lens.data_ptr(), 1.0 / math.sqrt(64))
-            return (lambda i: _rc(L, lib.zk_qkv_attn_f16_ln(*args, s())) and keep), \
+            tail = (part.data_ptr(), 1e-12, sc.data_ptr(), cc.data_ptr(), mr.data_ptr(),
+                    ctx.data_ptr(), B, S, H, heads, lens.data_ptr(), 1.0 / math.sqrt(64))
+            if frag:
+                args = (x.data_ptr(), w.data_ptr(), None) + tail
+                fn = lib.zk_qkv_attn_f16_frag
+            else:
+                args = (x.data_ptr(), w.data_ptr()) + tail
+                fn = lib.zk_qkv_attn_f16_ln
+            return (lambda i: _rc(L, fn(*args, s())) and keep), \
                 2.0 * B * S * 3 * H * H + 4.0 * B * heads * S * S * 64, "TFLOP/s", "fp16", "mfma", \
-                f"B={B} S={S} heads={heads} + attention (dense FLOPs), LayerNorm folded"
+                f"B={B} S={S} heads={heads} + attention (dense FLOPs), LayerNorm folded" + \
+                (", output in fragment order" if frag else "")
         return setup
 
     def add_ln(M=4096):
@@ -521,6 +553,8 @@ def kernel_cases(torch, dev):
         "ffn_down_res_stats": res_stats(4096, 3072, 768, pad=FFN_PAD),
         # the same two with the intermediate in fragment order, as the
         # encoder runs them at b32 s128
+        "qkv_attn_ln_s128_frag": qkv_attn_ln(frag=True),
+        "out_proj_res_stats_frag": out_proj_frag(),
         "ffn_up_ln_frag": ffn_frag()[0],
         "ffn_down_res_stats_frag": ffn_frag()[1],
         "attn_s512": attn(512),
@@ -564,11 +598,12 @@ ATTN_COMPUTED = {
     "attn_s512": lambda: _attn_computed_flops(512),
     "qkv_attn_s128": lambda: _attn_computed_flops(128, proj=_QKV_FLOPS),
     "qkv_attn_ln_s128": lambda: _attn_computed_flops(128, proj=_QKV_FLOPS),
+    "qkv_attn_ln_s128_frag": lambda: _attn_computed_flops(128, proj=_QKV_FLOPS),
 }
 
 # kernels one step of the timed encoder (b32 s128) launches, per layer: the
 # roofline line names the longest of them
-STEP_KERNELS = ("qkv_attn_ln_s128", "out_proj_res_stats", "ffn_up_ln_frag",
+STEP_KERNELS = ("qkv_attn_ln_s128_frag", "out_proj_res_stats_frag", "ffn_up_ln_frag",
                 "ffn_down_res_stats_frag")
 KERNEL_DESC = {
     "gemm_qkv": "gemm_mfma_kernel<F16Op, bias> M=4096 K=768 N=2304 (QKV)",
@@ -585,6 +620,11 @@ KERNEL_DESC = {
     "ffn_up_ln": "gemm_mfma_kernel<F16Op, folded LayerNorm + erf-GELU> M=4096 K=768 N=3072 (FFN-up)",
     "ffn_down_res_stats": "gemm_mfma_kernel<F16Op, bias + LayerNorm-ed residual + row statistics> "
                           "M=4096 K=3072 N=768 (FFN-down)",
+    "qkv_attn_ln_s128_frag": "gemm_mfma_kernel<F16Op, QKV + attention epilogue, folded LayerNorm, "
+                             "fragment-ordered output> M=4096 K=768 N=2304 + attention B=32 H=12 "
+                             "S=128 D=64",
+    "out_proj_res_stats_frag": "gemm_mfma_kernel<F16Op, fragment-ordered A, bias + LayerNorm-ed "
+                               "residual + row statistics> M=4096 K=768 N=768 (out-projection)",
     "ffn_up_ln_frag": "gemm_mfma_kernel<F16Op, folded LayerNorm + erf-GELU, fragment-ordered "
                       "output> M=4096 K=768 N=3072 (FFN-up)",
     "ffn_down_res_stats_frag": "gemm_mfma_kernel<F16Op, fragment-ordered A, bias + LayerNorm-ed "

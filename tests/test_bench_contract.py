@@ -12,7 +12,8 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 # every kernel an encoder layer launches (the roofline candidates), the
 # bandwidth-bound kernels held to the HBM target, and their same-byte copies
 PROFILED = ("qkv_attn_ln_s128", "out_proj_res_stats", "ffn_up_ln", "ffn_down_res_stats",
-            "ffn_up_ln_frag", "ffn_down_res_stats_frag",
+            "ffn_up_ln_frag", "ffn_down_res_stats_frag", "qkv_attn_ln_s128_frag",
+            "out_proj_res_stats_frag", "int8_ffn_up_frag", "int8_ffn_down_res_stats_frag",
             "int8_ffn_down_res_stats", "add_layernorm_q8_res_ln", "attn_s512",
             "add_layernorm", "add_layernorm_s512", "bias_gelu", "bias_gelu_s512",
             "copy_18.9MB", "copy_50.3MB", "copy_75.5MB", "copy_201MB")
