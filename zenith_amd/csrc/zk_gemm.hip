@@ -457,7 +457,8 @@ void gemm_mfma_kernel(GemmParams p) {
   const int kbytes = p.K * OP::kElem;
   const int64_t lda_b = p.lda * OP::kElem, ldb_b = p.ldb * OP::kElem;
   const int a_rows = min(BM, p.M - m0), b_rows = min(BN, p.N - n0);
-  // APK: the tile's row blocks of the fragment-ordered A, (K / 16) KB each
+  // APK: the tile's row blocks of the fragment-ordered A, one 1 KB fragment
+  // per 32 bytes of a row (kbytes / 32 KB each)
   const int a_blocks = min(BM / 32, (p.M + 31) / 32 - m0 / 32);
   const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
       APK ? (void *)((const char *)p.a_pk + (int64_t)(m0 / 32) * (kbytes / 32) * 1024)
