@@ -156,20 +156,25 @@ def test_frag_shape_errors(dev):
     torch.cuda.synchronize()
 
 
-def test_encoder_frag_ffn_bit_identical(dev):
+@pytest.mark.parametrize("B,S", [(32, 128), (33, 64), (17, 128)])
+def test_encoder_frag_ffn_bit_identical(dev, B, S):
+    """B x S rows: whole 256-row tiles (b32 s128), and ragged last tiles
+    (2112 and 2176 rows) whose fused-attention waves past the batch store
+    nothing."""
     layers = synthetic.bert_weights_wired(3, seed=7)
-    B, S = 32, 128
     x = torch.from_numpy(synthetic.hidden_states(B, S, seed=7)).to(dev, torch.float16)
     lens = torch.from_numpy(synthetic.padding_lengths(B, S)).to(dev)
     outs = []
+    print(f"encoder fragment order on/off B={B} S={S}", flush=True)
     for frag in (True, False):
         enc = BertEncoder(layers, device=dev)
         enc.ffn_frag = frag
+        enc.attn_frag = frag
         assert enc.frag_ffn(B * S) == frag
         outs.append(enc.forward(x, lens).clone())
         torch.cuda.synchronize()
         if frag:
-            assert enc._bufs["u_frag"] is not None
+            assert enc._bufs["u_frag"] is not None and enc._bufs["ctx_frag"] is not None
         del enc
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
 
