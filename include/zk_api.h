@@ -274,6 +274,14 @@ int zk_gemm_f16_ln_frag(const void *A, const void *W, void *C, int64_t M, int64_
  * are zk_gemm_f16_res_stats's, bit for bit, wherever that takes the same
  * tile (M < 10240 at N = 768). No reference counterpart (see
  * zk_gemm_f16_ln_frag). */
+/* C[M,N] = A . W^T + bias, fp16 out (row-major), A in fragment order
+ * (ceil(M/32) * 32 x K; rows past M read and discarded; K a multiple of 64):
+ * the INT8-FFN layer's out-projection on the fused attention's output. The
+ * 128x96 tile at every M. No reference counterpart (the out-projection
+ * linear_fp16_gpu, benchmarks/bert_fp16_full.py:124-126, on this layout). */
+int zk_gemm_f16_frag(const void *A, const void *W, void *C, int64_t M, int64_t N, int64_t K,
+                     int64_t ldw, int64_t ldc, const void *bias, void *stream);
+
 int zk_gemm_f16_res_stats_frag(const void *A, const void *W, void *C, int64_t M, int64_t N,
                                int64_t K, int64_t ldw, int64_t ldc, const void *bias,
                                const void *res, int64_t ldr, const float *res_ln,

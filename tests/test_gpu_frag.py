@@ -294,3 +294,33 @@ def test_qkv_attn_frag_matches_row_major(dev, B, S, ln):
     if Mp > M:
         pad = c1.view(Mp // 32, H // 16, 2, 32, 8)[-1, :, :, M % 32:, :]
         assert bool((pad == 7.0).all())
+
+
+@pytest.mark.parametrize("M,K,N", [(4096, 3072, 768), (1000, 3072, 768), (4096, 768, 768)])
+def test_gemm_f16_frag(dev, M, K, N):
+    """zk_gemm_f16_frag (A in fragment order, bias, the 128x96 tile): bit for
+    bit with zk_gemm_f16 where that runs the same tile (K >= 2048 at
+    N <= 1024), and at the fp16 bar against the oracle at the out-projection
+    shape, where zk_gemm_f16 takes 64x64 tiles."""
+    a = synthetic.round_f16(synthetic.normal((M, K), tag=230))
+    w = synthetic.round_f16(synthetic.normal((N, K), tag=231, std=1.0 / math.sqrt(K)))
+    b = synthetic.round_f16(synthetic.normal((N,), tag=232, std=0.1))
+    ta, tw, tb = _t(a, dev), _t(w, dev), _t(b, dev)
+    af = to_fragment_order(ta)
+    Mp = -(-M // 32) * 32
+    if Mp > M:
+        af.view(Mp // 32, K // 16, 2, 32, 8)[-1, :, :, M % 32:, :] = float("nan")
+    c0 = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+    c1 = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+    print(f"zk_gemm_f16_frag M={M} K={K} N={N}", flush=True)
+    L.call("zk_gemm_f16", ta.data_ptr(), tw.data_ptr(), c0.data_ptr(), M, N, K, K, K, N, 1,
+           L.ZK_F16, tb.data_ptr(), None, 0, L.ZK_EPI_BIAS, _stream())
+    L.call("zk_gemm_f16_frag", af.data_ptr(), tw.data_ptr(), c1.data_ptr(), M, N, K, K, N,
+           tb.data_ptr(), _stream())
+    torch.cuda.synchronize()
+    assert not torch.isnan(c1).any()
+    if K >= 2048:
+        assert torch.equal(c0.view(torch.int16), c1.view(torch.int16))
+    else:
+        ok, worst = fp16_tol(c1.float().cpu().numpy(), ops.linear(a, w, b))
+        assert ok, worst

@@ -65,6 +65,7 @@ SIGNATURES: dict[str, list] = {
                        _vp, _i32, _vp],
     "zk_gemm_f16_ln_frag": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _f32, _vp, _vp,
                             _vp, _vp],
+    "zk_gemm_f16_frag": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
     "zk_gemm_f16_res_stats_frag": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64,
                                    _vp, _vp, _vp, _vp, _vp],
     "zk_flash_attn_fwd": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,

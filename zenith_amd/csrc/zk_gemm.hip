@@ -1104,10 +1104,10 @@ static bool launch_epi(GemmParams p, int epi, hipStream_t s) {
 // The residual + statistics epilogue on fragment-ordered A (p.a_pk): the
 // fp16 128x96 tile of 4 x 1 waves and 3-stage ring that FFN-down runs on
 // with row-major A.
-template <class OP, bool DEQ>
+template <class OP, bool DEQ, int EPI = kEpiResStats>
 static void launch_frag_res_stats(GemmParams p, hipStream_t s) {
   const int grid = tile_grid(p, 128, 96);
-  gemm_mfma_kernel<OP, 128, 96, 32, 128, 3, 4, 1, kEpiResStats, f16, DEQ, true>
+  gemm_mfma_kernel<OP, 128, 96, 32, 128, 3, 4, 1, EPI, f16, DEQ, true>
       <<<grid, 256, 0, s>>>(p);
 }
 
@@ -1686,6 +1686,21 @@ extern "C" int zk_gemm_f16_res_stats(const void *A, const void *W, void *C, int6
   if (M == 0 || N == 0) return ZK_OK;
   GemmParams p{A, W, C, (int)M, (int)N, (int)K, lda, ldw, ldc, bias, res, ldr, 1.f, nullptr, 0};
   return res_stats_run<F16Op, false>(who, p, res_ln, res_gamma, res_beta, part_out, stream);
+}
+
+extern "C" int zk_gemm_f16_frag(const void *A, const void *W, void *C, int64_t M, int64_t N,
+                                int64_t K, int64_t ldw, int64_t ldc, const void *bias,
+                                void *stream) {
+  const char *who = "zk_gemm_f16_frag";
+  int st = check_ln_gemm(who, A, W, C, M, N, K, K, ldw, ldc);
+  if (st) return st;
+  if (M == 0 || N == 0) return ZK_OK;
+  if (K % 64) return fail(ZK_ERR_UNSUPPORTED, "%s: K must be a multiple of 64", who);
+  if (!bias) return fail(ZK_ERR_INVALID, "%s: null bias", who);
+  GemmParams p{A, W, C, (int)M, (int)N, (int)K, K, ldw, ldc, bias, nullptr, 0, 1.f, nullptr, 0};
+  p.a_pk = A;
+  launch_frag_res_stats<F16Op, false, ZK_EPI_BIAS>(p, as_stream(stream));
+  return check_launch(who);
 }
 
 extern "C" int zk_gemm_f16_res_stats_frag(const void *A, const void *W, void *C, int64_t M,

@@ -420,7 +420,7 @@ class BertEncoder:
             prev = None if first else self.layers[i - 1]
             h2, p2 = (bf["ping"], bf["p2a"]) if i % 2 == 0 else (bf["pong"], bf["p2b"])
             # 1-2. QKV projection (+ LN2 of the previous layer) and attention
-            cf = bf.get("ctx_frag") if self.int8 is None else None
+            cf = bf.get("ctx_frag")
             if cf is not None:
                 # ctx in fragment order for the out-projection below
                 L.call("zk_qkv_attn_f16_frag", cur.data_ptr(),
@@ -488,7 +488,11 @@ class BertEncoder:
                 # copy for FFN-up; LN2 stays folded as in the fp16 layer.
                 q, qh, qu, t = self.int8[i], bf["q_h"], bf["q_u"], bf["t"]
                 # 3. out-projection + bias -> t
-                self._gemm(ctx, w["Wo"], w["bo"], t, L.ZK_EPI_BIAS, stream=stream)
+                if cf is not None:
+                    L.call("zk_gemm_f16_frag", cf.data_ptr(), w["Wo"].data_ptr(), t.data_ptr(),
+                           M, H, H, H, H, w["bo"].data_ptr(), stream)
+                else:
+                    self._gemm(ctx, w["Wo"], w["bo"], t, L.ZK_EPI_BIAS, stream=stream)
                 # 4. h = LN1(t + the input, or + LN2(input) on the fly), and q(h)
                 if first:
                     L.call("zk_layernorm_q8", t.data_ptr(), cur.data_ptr(), w["ln1_g"].data_ptr(),
