@@ -121,6 +121,13 @@ def test_library_exports_every_declared_symbol():
                                          None), L.ZK_ERR_UNSUPPORTED),  # N a multiple of 64
     (lambda lib: lib.zk_gemm_i8_requant_frag(16, 16, 16, 8, 64, 64, 64, 64, 1.0, 16, 16, 2, 1.0,
                                              None), L.ZK_ERR_UNSUPPORTED),  # N % 128
+    (lambda lib: lib.zk_gemm_f16_frag(16, 16, 16, 8, 96, 96, 96, 96, 16, None),
+     L.ZK_ERR_UNSUPPORTED),  # fragment-ordered A: K a multiple of 64
+    (lambda lib: lib.zk_gemm_f16_frag(16, 16, 16, 8, 96, 128, 128, 96, None, None),
+     L.ZK_ERR_INVALID),  # no bias
+    (lambda lib: lib.zk_qkv_attn_f16_frag(16, 16, 16, None, 1e-12, None, None, None, 8, 2, 128,
+                                          768, 12, None, 0.125, None),
+     L.ZK_ERR_UNSUPPORTED),  # fragment-ordered ctx must be 16-byte aligned
     (lambda lib: lib.zk_gemm_i8_res_stats_frag(16, 16, 16, 8, 96, 64, 64, 96, 1.0, 16, 16, 16, 96,
                                                None, None, None, 16, None),
      L.ZK_ERR_UNSUPPORTED),  # fragment-ordered int8 A: K % 128
